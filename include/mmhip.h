@@ -1,0 +1,269 @@
+/*
+ * libmmhip: MI355X (gfx950) backend for the quantized-weight matrix path of
+ * mobile-moe.zig — Q8_0 / IQ2_XXS dequantisation, decode GEMV, batched QMM
+ * and the MoE expert FFN — behind a plain C ABI.
+ *
+ * Conventions follow the reference's C bridge (src/metal_bridge.c:50-87,
+ * src/metal_backend.zig:7-46): opaque handles, int status (0 = ok, < 0 =
+ * error), and a last-error string. The error string is thread-local here
+ * because the reference re-enters its seam from 4 pool workers
+ * (src/inference.zig:934-971).
+ *
+ * Pointers named *_host are ordinary host memory; pointers named *_dev are
+ * device memory (e.g. from mmhip_malloc). Every *_dev entry point is
+ * asynchronous on the context's stream (mmhip_stream); every host-slice
+ * entry point is synchronous, like OpenCLBackend's calls that end in
+ * clFinish (src/opencl_backend.zig:452).
+ *
+ * Tensor types use GgmlType ids (src/gguf.zig:21-56). Quantised weights are
+ * passed as raw GGUF bytes: Q8_0 blocks {f16 d; i8 qs[32]} (34 B,
+ * src/dequant.zig:372-377) and IQ2_XXS superblocks {f16 d; u16 qs[32]}
+ * (66 B, src/dequant.zig:305-311), row-major, rows of ceil(cols/bs) blocks.
+ * Uploading converts them once into the device tile layout the kernels read;
+ * the bytes per block stay the same.
+ *
+ * There is no CPU fallback anywhere in this library: without a usable HIP
+ * device every compute entry point returns MMHIP_ERR_UNAVAILABLE. The
+ * caller's engine decides what to do then (the reference falls back to its
+ * own CPU kernels at src/inference.zig:1209-1213).
+ */
+#ifndef MMHIP_H
+#define MMHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define MMHIP_OK 0
+#define MMHIP_ERR_UNAVAILABLE (-1) /* no HIP device / runtime */
+#define MMHIP_ERR_INVALID (-2)     /* bad argument or shape */
+#define MMHIP_ERR_UNSUPPORTED (-3) /* tensor type not on this path */
+#define MMHIP_ERR_HIP (-4)         /* HIP runtime error (see last error) */
+#define MMHIP_ERR_NOMEM (-5)
+
+/* ---- GgmlType ids (src/gguf.zig:21-56) ---- */
+#define MMHIP_TYPE_F32 0u
+#define MMHIP_TYPE_F16 1u
+#define MMHIP_TYPE_Q8_0 8u
+#define MMHIP_TYPE_IQ2_XXS 16u
+
+typedef struct mmhip_ctx mmhip_ctx;
+typedef struct mmhip_weight mmhip_weight;
+typedef struct mmhip_moe_layer mmhip_moe_layer;
+
+/* ======================================================================
+ * Backend object: replaces OpenCLBackend's lifecycle
+ * (src/opencl_backend.zig:92-300) and metal_init / metal_get_last_error
+ * (src/metal_bridge.c:52-87).
+ * ====================================================================== */
+
+/* Last error message of the calling thread ("" if none). */
+const char* mmhip_last_error(void);
+/* 1 if a gfx950 device is usable (OpenCLBackend.isAvailable, 92-99). */
+int mmhip_is_available(void);
+/* Number of visible HIP devices (0 if the runtime is absent). */
+int mmhip_device_count(void);
+/* Library build identifier (static string). */
+const char* mmhip_version(void);
+
+/* OpenCLBackend.init (101-281): create a context on `device`. */
+int mmhip_init(mmhip_ctx** out_ctx, int device);
+/* OpenCLBackend.deinit (283-300): frees every resident weight. */
+void mmhip_destroy(mmhip_ctx* ctx);
+/* Wait for all work queued on the context's stream (clFinish). */
+int mmhip_synchronize(mmhip_ctx* ctx);
+/* The context's hipStream_t, as an opaque pointer. */
+void* mmhip_stream(mmhip_ctx* ctx);
+/* Number of compute units of the context's device. */
+int mmhip_num_cu(mmhip_ctx* ctx);
+
+/* Kernel timing: when enabled, HIP events are recorded on the context's
+ * stream around every launch of the hot kernels; mmhip_profile_read sums
+ * them per kernel family ("gemv_q", "gemv_float", "qmm", "quantize",
+ * "moe_router", "moe_gateup", "moe_down", "moe_combine"). This fills the role
+ * of the per-op GPU timings the reference leaves empty
+ * (op_perf_db.zig:88-97). Enabling resets the accumulators. */
+int mmhip_profile_enable(mmhip_ctx* ctx, int enable);
+int mmhip_profile_read(mmhip_ctx* ctx, const char* family, double* total_ms, uint64_t* launches);
+
+/* Device memory helpers, so callers need no other HIP binding. */
+int mmhip_malloc(mmhip_ctx* ctx, void** out_dev, size_t bytes);
+int mmhip_free(mmhip_ctx* ctx, void* dev);
+int mmhip_memcpy_h2d(mmhip_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes);
+int mmhip_memcpy_d2h(mmhip_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes);
+int mmhip_memset_dev(mmhip_ctx* ctx, void* dst_dev, int value, size_t bytes);
+
+/* ======================================================================
+ * Device-resident weights: replaces getOrUploadMatBuffer's residency cache
+ * (src/opencl_backend.zig:311-323) with explicit handles.
+ * `count` stacks matrices of [rows x cols] back to back, as the expert
+ * tensors ffn_{gate,up,down}_exps are stored ([n_experts][rows][cols],
+ * src/inference.zig:1148-1166).
+ * ====================================================================== */
+
+int mmhip_weight_upload(mmhip_ctx* ctx, const void* raw_host, uint32_t type,
+                        uint64_t rows, uint64_t cols, uint64_t count,
+                        mmhip_weight** out_w);
+/* Same, from raw GGUF bytes already in device memory (not retained). */
+int mmhip_weight_from_device(mmhip_ctx* ctx, const void* raw_dev, uint32_t type,
+                             uint64_t rows, uint64_t cols, uint64_t count,
+                             mmhip_weight** out_w);
+void mmhip_weight_free(mmhip_ctx* ctx, mmhip_weight* w);
+/* Device bytes held by the weight (tile records + scales). */
+uint64_t mmhip_weight_device_bytes(const mmhip_weight* w);
+
+/* ======================================================================
+ * Engine seam, host slices. These replace the bodies of
+ *   matVecMulUnified   (src/inference.zig:1200-1228)
+ *   batchMatMulUnified (src/inference.zig:1231-1264)
+ *   dequant.dequantize (src/dequant.zig:632-659)
+ * and OpenCLBackend.matMulQ8_0 (src/opencl_backend.zig:412-453). The weight
+ * is uploaded on first use and kept resident, keyed by (ptr, type, shape).
+ * Supported types: F32, F16, Q8_0, IQ2_XXS.
+ * ====================================================================== */
+
+int mmhip_mat_vec_mul(mmhip_ctx* ctx, float* out_host, const void* ptr_host,
+                      uint32_t type, const float* x_host, uint64_t out_dim,
+                      uint64_t in_dim);
+/* out [batch][out_dim] = in [batch][in_dim] . W^T (the seam's layout). */
+int mmhip_batch_mat_mul(mmhip_ctx* ctx, float* out_host, const void* ptr_host,
+                        uint32_t type, const float* in_host, uint64_t out_dim,
+                        uint64_t batch, uint64_t in_dim);
+int mmhip_dequantize(mmhip_ctx* ctx, float* out_host, const void* data_host,
+                     uint32_t type, uint64_t n_elements);
+/* Drop the resident copy keyed by ptr_host (all types/shapes). */
+int mmhip_forget(mmhip_ctx* ctx, const void* ptr_host);
+
+/* ======================================================================
+ * Device twins (asynchronous on mmhip_stream(ctx)).
+ * ====================================================================== */
+
+/* dequantize from raw GGUF bytes in device memory; bit-exact. */
+int mmhip_dequantize_dev(mmhip_ctx* ctx, float* out_dev, const void* raw_dev,
+                         uint32_t type, uint64_t n_elements);
+/* y[rows] = W[mat] . x[cols] for one matrix of a weight. */
+int mmhip_gemv_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat,
+                   const float* x_dev, float* y_dev);
+/* n_mats products in ONE launch: y_i = W[first + i] . x_i with
+ * x_i = x_dev + i * x_stride, y_i = y_dev + i * y_stride (strides in
+ * floats; x_stride 0 shares one input vector). */
+int mmhip_gemv_batched_dev(mmhip_ctx* ctx, const mmhip_weight* w,
+                           uint64_t first, uint64_t n_mats,
+                           const float* x_dev, uint64_t x_stride,
+                           float* y_dev, uint64_t y_stride);
+/* Batched QMM for prompt prefill: X [batch][cols] -> Y.
+ * out_layout 0: Y [batch][rows] (batchMatMulUnified's layout);
+ * out_layout 1: Y [rows][batch] (qmm.matMulQ8_0's layout, qmm.zig:52-57). */
+int mmhip_qmm_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat,
+                  const float* x_dev, float* y_dev, uint64_t batch,
+                  int out_layout);
+
+/* ======================================================================
+ * MoE FFN layer: replaces moeFFN (src/inference.zig:886-1010) with
+ * expertFFN (1152-1188), sharedExpertFFN (1094-1146), Scheduler.route
+ * (src/scheduler.zig:169-262) and the per-token batch loop of forwardBatch
+ * (src/inference.zig:346-351). Routing, expert FFNs, the weighted sum and
+ * the shared expert all run on the device; nothing is copied back between
+ * steps.
+ * ====================================================================== */
+
+typedef struct {
+    uint32_t hidden_size;          /* hp.hidden_size (2048) */
+    uint32_t moe_intermediate;     /* hp.moe_intermediate_size (1536) */
+    uint32_t shared_intermediate;  /* width of the shared expert */
+    uint32_t n_routed_experts;     /* hp.n_routed_experts (64) */
+    uint32_t expert_type;          /* lw.expert_type (Q8_0 or IQ2_XXS) */
+    uint32_t shared_type;          /* lw.shared_type */
+    uint32_t router_type;          /* lw.moe_gate_type (F32 or F16) */
+    float routed_scaling_factor;   /* hp.routed_scaling_factor */
+    const void* router_host;       /* [n_experts][hidden] */
+    const void* expert_gate_host;  /* [n_experts][moe_inter][hidden] */
+    const void* expert_up_host;    /* [n_experts][moe_inter][hidden] */
+    const void* expert_down_host;  /* [n_experts][hidden][moe_inter] */
+    const void* shared_gate_host;  /* [shared_inter][hidden], NULL = none */
+    const void* shared_up_host;
+    const void* shared_down_host;  /* [hidden][shared_inter] */
+} mmhip_moe_weights;
+
+/* Throttle inputs of Scheduler.route (ThrottleState fields,
+ * src/thermal.zig:17-72). level: 0 normal, 1 light, 2 medium, 3 heavy. */
+typedef struct {
+    int32_t throttle_level;
+    uint32_t active_expert_limit;  /* 0 = the level's default (4/3/2/1) */
+    const float* deferral_bias_host; /* [hidden] or NULL (Scheduler.deferral_bias) */
+} mmhip_route_params;
+
+#define MMHIP_MOE_MAX_TOKENS 256u  /* forwardBatch's max_batch_size (inference.zig:115) */
+
+int mmhip_moe_layer_create(mmhip_ctx* ctx, const mmhip_moe_weights* wts,
+                           mmhip_moe_layer** out_layer);
+void mmhip_moe_layer_destroy(mmhip_ctx* ctx, mmhip_moe_layer* layer);
+
+/* n_tokens hidden vectors in, n_tokens FFN outputs out (host buffers,
+ * synchronous). route_ids / route_weights (optional, [n_tokens][4]) receive
+ * Scheduler.route's expert_ids / weights; unused slots hold 0xFFFFFFFF / 0.
+ * Returns k (experts per token) or < 0. */
+int mmhip_moe_ffn(mmhip_ctx* ctx, mmhip_moe_layer* layer, const float* hidden_host,
+                  float* out_host, uint32_t n_tokens, const mmhip_route_params* rp,
+                  uint32_t* route_ids_host, float* route_weights_host);
+/* Device twin (asynchronous). route_*_dev may be NULL. Returns 0 or < 0. */
+int mmhip_moe_ffn_dev(mmhip_ctx* ctx, mmhip_moe_layer* layer, const float* hidden_dev,
+                      float* out_dev, uint32_t n_tokens, const mmhip_route_params* rp,
+                      uint32_t* route_ids_dev, float* route_weights_dev);
+/* ExpertStats.counts for this layer (scheduler.zig:19-44): activations per
+ * expert since creation, [n_routed_experts]. Synchronous. */
+int mmhip_moe_expert_counts(mmhip_ctx* ctx, mmhip_moe_layer* layer, uint64_t* counts_host);
+
+/* ======================================================================
+ * Operator planner: OpScheduler / LayerPlan (src/scheduler.zig:265-552)
+ * with the GPU rules this backend adds. Host logic only; no device needed.
+ * ====================================================================== */
+
+/* op_perf_db.OpType (src/op_perf_db.zig:26-40) */
+enum {
+    MMHIP_OP_MATMUL_Q8_0 = 0, MMHIP_OP_MATMUL_Q4_K, MMHIP_OP_MATMUL_F32,
+    MMHIP_OP_MATVEC_Q8_0, MMHIP_OP_MATVEC_F32, MMHIP_OP_RMSNORM,
+    MMHIP_OP_SILU_MUL, MMHIP_OP_ROPE, MMHIP_OP_SOFTMAX, MMHIP_OP_DOT,
+    MMHIP_OP_ATTENTION, MMHIP_OP_FFN_GATE_UP, MMHIP_OP_FFN_DOWN
+};
+/* op_perf_db.Precision (43-48) plus the iq2_xxs value this backend adds. */
+enum { MMHIP_PREC_Q8_0 = 0, MMHIP_PREC_Q4_K, MMHIP_PREC_F32, MMHIP_PREC_F16, MMHIP_PREC_IQ2_XXS };
+/* scheduler.Backend (268-272) */
+enum { MMHIP_BACKEND_CPU = 0, MMHIP_BACKEND_GPU = 1, MMHIP_BACKEND_NPU = 2 };
+
+typedef struct { uint32_t m, n, k, dim; } mmhip_shape;          /* op_perf_db.Shape */
+typedef struct {                                                /* OpSchedule (275-288) */
+    uint32_t op, backend, precision, sync_after;
+    mmhip_shape shape;
+    uint64_t estimated_us;
+} mmhip_op_schedule;
+typedef struct {                                                /* PlanHyperParams (544-552) */
+    uint32_t hidden_size, intermediate_size, num_heads, head_dim;
+    uint32_t seq_len_hint;          /* 0 = 128 */
+    uint32_t leading_dense_layers, n_routed_experts;
+    uint32_t weight_precision;      /* MMHIP_PREC_* of the FFN weights */
+} mmhip_plan_hparams;
+typedef struct {                                                /* OpPerfDb entry (88-97) */
+    uint32_t op, precision;
+    mmhip_shape shape;
+    uint64_t cpu_us, gpu_us;
+} mmhip_perf_entry;
+
+/* OpScheduler.init + planLayer (364-503). has_gpu normally comes from
+ * mmhip_is_available(). Writes up to `cap` schedules, *n_out = count. */
+int mmhip_plan_layer(uint32_t layer, const mmhip_plan_hparams* hp, int has_gpu,
+                     int has_npu, int throttle_level, const mmhip_perf_entry* db,
+                     size_t db_len, mmhip_op_schedule* out, size_t cap, size_t* n_out);
+/* LayerPlan.estimatedCriticalPathUs (313-333) */
+uint64_t mmhip_plan_critical_path_us(const mmhip_op_schedule* ops, size_t n);
+/* LayerPlan.deviceMask (336-346) */
+uint32_t mmhip_plan_device_mask(const mmhip_op_schedule* ops, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,354 @@
+// extern "C" surface of libmmhip (declared in include/mmhip.h): context
+// lifecycle, device memory helpers, weight residency, and the engine-seam
+// entry points (matVecMulUnified / batchMatMulUnified / dequantize).
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/mmhip.h"
+#include "backend.hpp"
+
+namespace mmhip {
+const char* last_error_cstr();
+}
+
+using namespace mmhip;
+
+namespace {
+
+int require_ctx(mmhip_ctx* ctx) {
+    if (!ctx) {
+        set_error(MMHIP_ERR_INVALID, "null context");
+        return MMHIP_ERR_INVALID;
+    }
+    return MMHIP_OK;
+}
+
+bool gfx950_present(int* count_out) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) count = 0;
+    if (count_out) *count_out = count;
+    for (int d = 0; d < count; ++d) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, d) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+            return true;
+    }
+    return false;
+}
+
+// Resident weight for a host pointer (getOrUploadMatBuffer semantics).
+int resident_weight(mmhip_ctx* ctx, const void* ptr, uint32_t type, uint64_t rows, uint64_t cols,
+                    mmhip_weight** out) {
+    auto key = std::make_tuple(ptr, type, rows, cols);
+    auto it = ctx->resident.find(key);
+    if (it != ctx->resident.end()) {
+        *out = it->second;
+        return MMHIP_OK;
+    }
+    int rc = weight_create(ctx, ptr, false, type, rows, cols, 1, out);
+    if (rc == MMHIP_OK) ctx->resident[key] = *out;
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mmhip_last_error(void) { return last_error_cstr(); }
+
+const char* mmhip_version(void) { return "libmmhip 0.1 gfx950"; }
+
+int mmhip_device_count(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) return 0;
+    return count;
+}
+
+int mmhip_is_available(void) { return gfx950_present(nullptr) ? 1 : 0; }
+
+int mmhip_init(mmhip_ctx** out_ctx, int device) {
+    if (!out_ctx) {
+        set_error(MMHIP_ERR_INVALID, "init: null output pointer");
+        return MMHIP_ERR_INVALID;
+    }
+    *out_ctx = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+        set_error(MMHIP_ERR_UNAVAILABLE, "init: no HIP device");
+        return MMHIP_ERR_UNAVAILABLE;
+    }
+    if (device < 0 || device >= count) {
+        set_error(MMHIP_ERR_INVALID, "init: device index out of range");
+        return MMHIP_ERR_INVALID;
+    }
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(e, "init: hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_error(MMHIP_ERR_UNAVAILABLE, std::string("init: device is ") + prop.gcnArchName +
+                                             ", this library is built for gfx950 only");
+        return MMHIP_ERR_UNAVAILABLE;
+    }
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "init: hipSetDevice");
+    mmhip_ctx* ctx = new mmhip_ctx();
+    ctx->device = device;
+    ctx->num_cu = prop.multiProcessorCount;
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_fail(e, "init: hipStreamCreate");
+    }
+    uint32_t tables[kIq2TableWordsHost];
+    build_iq2_tables(tables);
+    e = hipMalloc(&ctx->iq2_tables, sizeof(tables));
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(ctx->iq2_tables, tables, sizeof(tables), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        mmhip_destroy(ctx);
+        return hip_fail(e, "init: tables");
+    }
+    *out_ctx = ctx;
+    return MMHIP_OK;
+}
+
+void mmhip_destroy(mmhip_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->resident) weight_destroy(kv.second);
+    ctx->resident.clear();
+    ctx->d_in.release();
+    ctx->d_out.release();
+    ctx->d_raw.release();
+    ctx->d_q.release();
+    ctx->h_in.release();
+    ctx->h_out.release();
+    if (ctx->iq2_tables) (void)hipFree(ctx->iq2_tables);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+int mmhip_synchronize(mmhip_ctx* ctx) {
+    if (int rc = require_ctx(ctx)) return rc;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "synchronize");
+}
+
+void* mmhip_stream(mmhip_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int mmhip_num_cu(mmhip_ctx* ctx) { return ctx ? ctx->num_cu : 0; }
+
+int mmhip_profile_enable(mmhip_ctx* ctx, int enable) {
+    if (int rc = require_ctx(ctx)) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    (void)hipStreamSynchronize(ctx->stream);
+    ctx->timer.reset();
+    ctx->timer.on = enable != 0;
+    return MMHIP_OK;
+}
+
+int mmhip_profile_read(mmhip_ctx* ctx, const char* family, double* total_ms, uint64_t* launches) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!family) {
+        set_error(MMHIP_ERR_INVALID, "profile_read: null family");
+        return MMHIP_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "profile_read");
+    ctx->timer.drain();
+    auto it = ctx->timer.totals.find(family);
+    if (total_ms) *total_ms = it == ctx->timer.totals.end() ? 0.0 : it->second.first;
+    if (launches) *launches = it == ctx->timer.totals.end() ? 0 : it->second.second;
+    return MMHIP_OK;
+}
+
+int mmhip_malloc(mmhip_ctx* ctx, void** out_dev, size_t bytes) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!out_dev) {
+        set_error(MMHIP_ERR_INVALID, "malloc: null output pointer");
+        return MMHIP_ERR_INVALID;
+    }
+    hipError_t e = hipMalloc(out_dev, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        *out_dev = nullptr;
+        set_error(MMHIP_ERR_NOMEM, std::string("malloc: ") + hipGetErrorString(e));
+        return MMHIP_ERR_NOMEM;
+    }
+    return MMHIP_OK;
+}
+
+int mmhip_free(mmhip_ctx* ctx, void* dev) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!dev) return MMHIP_OK;
+    hipError_t e = hipFree(dev);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "free");
+}
+
+int mmhip_memcpy_h2d(mmhip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (int rc = require_ctx(ctx)) return rc;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "memcpy_h2d");
+}
+
+int mmhip_memcpy_d2h(mmhip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (int rc = require_ctx(ctx)) return rc;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "memcpy_d2h");
+}
+
+int mmhip_memset_dev(mmhip_ctx* ctx, void* dst, int value, size_t bytes) {
+    if (int rc = require_ctx(ctx)) return rc;
+    hipError_t e = hipMemsetAsync(dst, value, bytes, ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "memset");
+}
+
+int mmhip_weight_upload(mmhip_ctx* ctx, const void* raw_host, uint32_t type, uint64_t rows, uint64_t cols,
+                        uint64_t count, mmhip_weight** out_w) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!raw_host || !out_w) {
+        set_error(MMHIP_ERR_INVALID, "weight_upload: null pointer");
+        return MMHIP_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    return weight_create(ctx, raw_host, false, type, rows, cols, count, out_w);
+}
+
+int mmhip_weight_from_device(mmhip_ctx* ctx, const void* raw_dev, uint32_t type, uint64_t rows, uint64_t cols,
+                             uint64_t count, mmhip_weight** out_w) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!raw_dev || !out_w) {
+        set_error(MMHIP_ERR_INVALID, "weight_from_device: null pointer");
+        return MMHIP_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    return weight_create(ctx, raw_dev, true, type, rows, cols, count, out_w);
+}
+
+void mmhip_weight_free(mmhip_ctx* ctx, mmhip_weight* w) {
+    if (!w) return;
+    if (ctx) (void)hipStreamSynchronize(ctx->stream);
+    weight_destroy(w);
+}
+
+uint64_t mmhip_weight_device_bytes(const mmhip_weight* w) { return w ? w->bytes : 0; }
+
+int mmhip_mat_vec_mul(mmhip_ctx* ctx, float* out, const void* ptr, uint32_t type, const float* x,
+                      uint64_t out_dim, uint64_t in_dim) {
+    return mmhip_batch_mat_mul(ctx, out, ptr, type, x, out_dim, 1, in_dim);
+}
+
+int mmhip_batch_mat_mul(mmhip_ctx* ctx, float* out, const void* ptr, uint32_t type, const float* in,
+                        uint64_t out_dim, uint64_t batch, uint64_t in_dim) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (batch == 0 || out_dim == 0) return MMHIP_OK;
+    if (!out || !ptr || !in || in_dim == 0) {
+        set_error(MMHIP_ERR_INVALID, "mat_mul: null pointer or zero in_dim");
+        return MMHIP_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    mmhip_weight* w = nullptr;
+    int rc = resident_weight(ctx, ptr, type, out_dim, in_dim, &w);
+    if (rc) return rc;
+    const size_t in_bytes = batch * in_dim * 4, out_bytes = batch * out_dim * 4;
+    hipError_t e = ctx->h_in.ensure(in_bytes);
+    if (e == hipSuccess) e = ctx->h_out.ensure(out_bytes);
+    if (e == hipSuccess) e = ctx->d_in.ensure(in_bytes);
+    if (e == hipSuccess) e = ctx->d_out.ensure(out_bytes);
+    if (e != hipSuccess) return hip_fail(e, "mat_mul: staging");
+    std::memcpy(ctx->h_in.p, in, in_bytes);
+    e = hipMemcpyAsync(ctx->d_in.p, ctx->h_in.p, in_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "mat_mul: H2D");
+    const float* dx = static_cast<const float*>(ctx->d_in.p);
+    float* dy = static_cast<float*>(ctx->d_out.p);
+    if (batch == 1)
+        rc = gemv_device(ctx, w, 0, 1, dx, 0, dy, 0, &ctx->d_q);
+    else
+        rc = qmm_device(ctx, w, 0, dx, dy, batch, 0, &ctx->d_q);
+    if (rc) return rc;
+    e = hipMemcpyAsync(ctx->h_out.p, dy, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "mat_mul: D2H");
+    std::memcpy(out, ctx->h_out.p, out_bytes);
+    return MMHIP_OK;
+}
+
+int mmhip_dequantize(mmhip_ctx* ctx, float* out, const void* data, uint32_t type, uint64_t n) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (n == 0) return MMHIP_OK;
+    if (!out || !data) {
+        set_error(MMHIP_ERR_INVALID, "dequantize: null pointer");
+        return MMHIP_ERR_INVALID;
+    }
+    const uint64_t raw_bytes = tensor_bytes(type, n);
+    if (raw_bytes == 0) {
+        set_error(MMHIP_ERR_UNSUPPORTED, "dequantize: unsupported GgmlType " + std::to_string(type));
+        return MMHIP_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipError_t e = ctx->d_raw.ensure(raw_bytes);
+    if (e == hipSuccess) e = ctx->d_out.ensure(n * 4);
+    if (e != hipSuccess) return hip_fail(e, "dequantize: scratch");
+    e = hipMemcpyAsync(ctx->d_raw.p, data, raw_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = launch_dequant(ctx->d_raw.p, type, n, static_cast<float*>(ctx->d_out.p), ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, ctx->d_out.p, n * 4, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "dequantize");
+}
+
+int mmhip_forget(mmhip_ctx* ctx, const void* ptr) {
+    if (int rc = require_ctx(ctx)) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto it = ctx->resident.begin(); it != ctx->resident.end();) {
+        if (std::get<0>(it->first) == ptr) {
+            weight_destroy(it->second);
+            it = ctx->resident.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    return MMHIP_OK;
+}
+
+int mmhip_dequantize_dev(mmhip_ctx* ctx, float* out_dev, const void* raw_dev, uint32_t type, uint64_t n) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (tensor_bytes(type, 1) == 0) {
+        set_error(MMHIP_ERR_UNSUPPORTED, "dequantize_dev: unsupported GgmlType " + std::to_string(type));
+        return MMHIP_ERR_UNSUPPORTED;
+    }
+    hipError_t e = launch_dequant(raw_dev, type, n, out_dev, ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "dequantize_dev");
+}
+
+int mmhip_gemv_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x_dev, float* y_dev) {
+    return mmhip_gemv_batched_dev(ctx, w, mat, 1, x_dev, 0, y_dev, 0);
+}
+
+int mmhip_gemv_batched_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t n_mats,
+                           const float* x_dev, uint64_t x_stride, float* y_dev, uint64_t y_stride) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!w || !x_dev || !y_dev) {
+        set_error(MMHIP_ERR_INVALID, "gemv_dev: null pointer");
+        return MMHIP_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    return gemv_device(ctx, w, first, n_mats, x_dev, x_stride, y_dev, y_stride, &ctx->d_q);
+}
+
+int mmhip_qmm_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x_dev, float* y_dev,
+                  uint64_t batch, int out_layout) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!w || !x_dev || !y_dev || (out_layout != 0 && out_layout != 1)) {
+        set_error(MMHIP_ERR_INVALID, "qmm_dev: null pointer or bad layout");
+        return MMHIP_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    return qmm_device(ctx, w, mat, x_dev, y_dev, batch, out_layout, &ctx->d_q);
+}
+
+}  // extern "C"

@@ -1,0 +1,386 @@
+// HipBackend internals: error state, scratch buffers, weight upload + repack,
+// and the device-pointer GEMV / QMM drivers used by every entry point.
+#include "backend.hpp"
+
+#include <cstring>
+#include <string>
+
+#include "../../include/mmhip.h"
+
+namespace mmhip {
+
+namespace {
+thread_local std::string t_err;
+}  // namespace
+
+const char* last_error_cstr() { return t_err.c_str(); }
+
+void set_error(int code, const std::string& msg) {
+    (void)code;
+    t_err = msg;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    set_error(MMHIP_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    return MMHIP_ERR_HIP;
+}
+
+uint64_t block_size(uint32_t type) {
+    switch (type) {
+        case kF32: case kF16: return 1;
+        case kQ8_0: return 32;
+        case kIq2Xxs: return 256;
+        default: return 0;
+    }
+}
+
+uint64_t block_bytes(uint32_t type) {
+    switch (type) {
+        case kF32: return 4;
+        case kF16: return 2;
+        case kQ8_0: return 34;
+        case kIq2Xxs: return 66;
+        default: return 0;
+    }
+}
+
+uint64_t tensor_bytes(uint32_t type, uint64_t n) {
+    const uint64_t bs = block_size(type);
+    if (bs == 0) return 0;
+    return ((n + bs - 1) / bs) * block_bytes(type);
+}
+
+hipError_t DevBuf::ensure(size_t bytes) {
+    if (bytes <= cap) return hipSuccess;
+    release();
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        p = nullptr;
+        return e;
+    }
+    cap = want;
+    return hipSuccess;
+}
+
+void DevBuf::release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+}
+
+hipError_t HostBuf::ensure(size_t bytes) {
+    if (bytes <= cap) return hipSuccess;
+    release();
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        p = nullptr;
+        return e;
+    }
+    cap = want;
+    return hipSuccess;
+}
+
+void HostBuf::release() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    cap = 0;
+}
+
+static uint64_t round_up(uint64_t v, uint64_t m) { return (v + m - 1) / m * m; }
+
+QuantAct quant_act_view(void* base, uint64_t n_vec, uint64_t cols_pad) {
+    const uint64_t stride = round_up(cols_pad, 64);
+    QuantAct q;
+    q.hi = static_cast<int8_t*>(base);
+    q.lo = q.hi + n_vec * stride;
+    q.scale = reinterpret_cast<float*>(q.lo + n_vec * stride);
+    q.stride = stride;
+    q.scale_stride = stride / 32;
+    return q;
+}
+
+size_t quant_act_bytes(uint64_t n_vec, uint64_t cols_pad) {
+    const uint64_t stride = round_up(cols_pad, 64);
+    return (size_t)(2 * n_vec * stride + n_vec * (stride / 32) * 4);
+}
+
+// Builds the IQ2_XXS LDS tables (layout in kernels/device_common.hpp):
+//   LO[idx * 16 + (b012 | P << 3)]       columns 0..3, sign bits b0 b1 b2 b3,
+//                                        b3 = P ^ parity(b012)
+//   HI[hi3 * 512 + idx * 2 + P]          columns 4..7, sign bits hi3 (4..6) and
+//                                        bit 7 = P ^ parity(hi3)
+// Each entry packs four signed int8 weights grid_byte * (+-1).
+void build_iq2_tables(uint32_t* out) {
+    static const uint64_t grid[256] = {
+#include "iq2xxs_grid.inc"
+    };
+    auto pack = [](uint64_t g, int first, uint32_t signs) {
+        uint32_t word = 0;
+        for (int j = 0; j < 4; ++j) {
+            int v = (int)((g >> (8 * (first + j))) & 0xFFu);
+            if ((signs >> j) & 1u) v = -v;
+            word |= (uint32_t)(uint8_t)(int8_t)v << (8 * j);
+        }
+        return word;
+    };
+    for (uint32_t idx = 0; idx < 256; ++idx) {
+        for (uint32_t e = 0; e < 16; ++e) {
+            const uint32_t b012 = e & 7u, p = e >> 3;
+            const uint32_t b3 = p ^ (uint32_t)(__builtin_popcount(b012) & 1);
+            out[idx * 16 + e] = pack(grid[idx], 0, b012 | (b3 << 3));
+        }
+        for (uint32_t hi3 = 0; hi3 < 8; ++hi3) {
+            for (uint32_t p = 0; p < 2; ++p) {
+                const uint32_t b7 = p ^ (uint32_t)(__builtin_popcount(hi3) & 1);
+                out[4096 + hi3 * 512 + idx * 2 + p] = pack(grid[idx], 4, hi3 | (b7 << 3));
+            }
+        }
+    }
+}
+
+int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t type, uint64_t rows,
+                  uint64_t cols, uint64_t count, mmhip_weight** out) {
+    *out = nullptr;
+    if (rows == 0 || cols == 0 || count == 0) {
+        set_error(MMHIP_ERR_INVALID, "weight: rows, cols and count must be > 0");
+        return MMHIP_ERR_INVALID;
+    }
+    if (block_size(type) == 0) {
+        set_error(MMHIP_ERR_UNSUPPORTED, "weight: GgmlType " + std::to_string(type) +
+                                             " is not on this backend's path (F32, F16, Q8_0, IQ2_XXS)");
+        return MMHIP_ERR_UNSUPPORTED;
+    }
+    if (type == kIq2Xxs && cols % 256 != 0) {
+        set_error(MMHIP_ERR_INVALID, "weight: IQ2_XXS rows must hold whole 256-element superblocks");
+        return MMHIP_ERR_INVALID;
+    }
+    const uint64_t row_bytes = ((cols + block_size(type) - 1) / block_size(type)) * block_bytes(type);
+    const uint64_t raw_bytes = row_bytes * rows * count;
+    mmhip_weight* w = new mmhip_weight();
+    w->type = type;
+    w->rows = rows;
+    w->cols = cols;
+    w->count = count;
+    hipError_t e;
+    if (type == kF32 || type == kF16) {
+        e = hipMalloc(&w->plain, raw_bytes);
+        if (e != hipSuccess) {
+            delete w;
+            return hip_fail(e, "weight: hipMalloc");
+        }
+        w->bytes = raw_bytes;
+        e = hipMemcpyAsync(w->plain, raw, raw_bytes, raw_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                           ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            weight_destroy(w);
+            return hip_fail(e, "weight: upload");
+        }
+        *out = w;
+        return MMHIP_OK;
+    }
+    TileGeom& g = w->geom;
+    g.fmt = (type == kIq2Xxs) ? kFmtIq2 : kFmtQ8;
+    g.rows = rows;
+    g.cols = cols;
+    g.count = count;
+    g.tiles = (rows + 15) / 16;
+    g.unit_cols = (type == kIq2Xxs) ? 256 : 64;
+    g.units = (type == kIq2Xxs) ? cols / 256 : ((cols + 31) / 32 + 1) / 2;
+    g.cols_pad = g.units * g.unit_cols;
+    g.rec_stride = g.tiles * g.units * 64;
+    g.d_stride = g.tiles * g.units * ((type == kIq2Xxs) ? 16 : 32);
+    const size_t rec_bytes = (size_t)(g.rec_stride * count * 16);
+    const size_t d_bytes = (size_t)(g.d_stride * count * 2);
+    e = hipMalloc(&w->recs, rec_bytes);
+    if (e == hipSuccess) e = hipMalloc(&w->dvals, d_bytes);
+    if (e != hipSuccess) {
+        weight_destroy(w);
+        return hip_fail(e, "weight: hipMalloc");
+    }
+    w->bytes = rec_bytes + d_bytes;
+    const void* src = raw;
+    if (!raw_on_device) {
+        e = ctx->d_raw.ensure(raw_bytes);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(ctx->d_raw.p, raw, raw_bytes, hipMemcpyHostToDevice, ctx->stream);
+        if (e != hipSuccess) {
+            weight_destroy(w);
+            return hip_fail(e, "weight: upload");
+        }
+        src = ctx->d_raw.p;
+    }
+    e = launch_repack(src, g, w->recs, w->dvals, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        weight_destroy(w);
+        return hip_fail(e, "weight: repack");
+    }
+    *out = w;
+    return MMHIP_OK;
+}
+
+void weight_destroy(mmhip_weight* w) {
+    if (!w) return;
+    if (w->recs) (void)hipFree(w->recs);
+    if (w->dvals) (void)hipFree(w->dvals);
+    if (w->plain) (void)hipFree(w->plain);
+    delete w;
+}
+
+int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t n, const float* x,
+                uint64_t x_stride, float* y, uint64_t y_stride, DevBuf* qscratch) {
+    if (n == 0) return MMHIP_OK;
+    if (first + n > w->count) {
+        set_error(MMHIP_ERR_INVALID, "gemv: matrix index out of range");
+        return MMHIP_ERR_INVALID;
+    }
+    hipError_t e;
+    if (w->type == kF32 || w->type == kF16) {
+        const uint64_t es = (w->type == kF32) ? 4 : 2;
+        const uint64_t mstride = w->rows * w->cols;
+        const char* base = static_cast<const char*>(w->plain) + first * mstride * es;
+        {
+            TimedLaunch tl(ctx, "gemv_float");
+            e = launch_gemv_float(base, w->type, mstride, x, x_stride, y, y_stride, (uint32_t)n, (uint32_t)w->rows,
+                                  (uint32_t)w->cols, ctx->stream);
+        }
+        return e == hipSuccess ? MMHIP_OK : hip_fail(e, "gemv: launch");
+    }
+    const TileGeom& g = w->geom;
+    const uint64_t nvec = x_stride ? n : 1;
+    e = qscratch->ensure(quant_act_bytes(nvec, g.cols_pad));
+    if (e != hipSuccess) return hip_fail(e, "gemv: scratch");
+    QuantAct q = quant_act_view(qscratch->p, nvec, g.cols_pad);
+    {
+        TimedLaunch tl(ctx, "quantize");
+        e = launch_quantize(x, x_stride, (uint32_t)nvec, (uint32_t)w->cols, (uint32_t)g.cols_pad, q, ctx->stream);
+    }
+    if (e != hipSuccess) return hip_fail(e, "gemv: quantize");
+    GemvArgs a;
+    a.recs = w->recs;
+    a.dvals = w->dvals;
+    a.rec_stride = g.rec_stride;
+    a.d_stride = g.d_stride;
+    a.xh = q.hi;
+    a.xl = q.lo;
+    a.xs = q.scale;
+    a.xq_stride = x_stride ? q.stride : 0;
+    a.xs_stride = x_stride ? q.scale_stride : 0;
+    a.y = y;
+    a.y_stride = y_stride;
+    a.tables = ctx->iq2_tables;
+    a.first_mat = first;
+    a.n_probs = (uint32_t)n;
+    a.tiles = (uint32_t)g.tiles;
+    a.units = (uint32_t)g.units;
+    a.rows = (uint32_t)g.rows;
+    {
+        TimedLaunch tl(ctx, "gemv_q");
+        e = launch_gemv_q(a, g.fmt, ctx->num_cu, ctx->stream);
+    }
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "gemv: launch");
+}
+
+int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y, uint64_t batch,
+               int out_layout, DevBuf* qscratch) {
+    if (batch == 0) return MMHIP_OK;
+    if (mat >= w->count) {
+        set_error(MMHIP_ERR_INVALID, "qmm: matrix index out of range");
+        return MMHIP_ERR_INVALID;
+    }
+    hipError_t e;
+    if (w->type == kF32 || w->type == kF16) {
+        if (out_layout != 0) {
+            set_error(MMHIP_ERR_UNSUPPORTED, "qmm: float weights support out_layout 0 only");
+            return MMHIP_ERR_UNSUPPORTED;
+        }
+        const uint64_t es = (w->type == kF32) ? 4 : 2;
+        const char* base = static_cast<const char*>(w->plain) + mat * w->rows * w->cols * es;
+        e = launch_gemv_float(base, w->type, 0, x, w->cols, y, w->rows, (uint32_t)batch, (uint32_t)w->rows,
+                              (uint32_t)w->cols, ctx->stream);
+        return e == hipSuccess ? MMHIP_OK : hip_fail(e, "qmm: launch");
+    }
+    const TileGeom& g = w->geom;
+    e = qscratch->ensure(quant_act_bytes(batch, g.cols_pad));
+    if (e != hipSuccess) return hip_fail(e, "qmm: scratch");
+    QuantAct q = quant_act_view(qscratch->p, batch, g.cols_pad);
+    {
+        TimedLaunch tl(ctx, "quantize");
+        e = launch_quantize(x, w->cols, (uint32_t)batch, (uint32_t)w->cols, (uint32_t)g.cols_pad, q, ctx->stream);
+    }
+    if (e != hipSuccess) return hip_fail(e, "qmm: quantize");
+    const uint64_t ld = out_layout == 0 ? w->rows : batch;
+    {
+        TimedLaunch tl(ctx, "qmm");
+        e = launch_qmm(w->recs, w->dvals, g, mat, q, (uint32_t)batch, y, ld, out_layout, ctx->iq2_tables,
+                       ctx->stream);
+    }
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "qmm: launch");
+}
+
+}  // namespace mmhip
+
+hipEvent_t KernelTimer::get() {
+    if (!pool.empty()) {
+        hipEvent_t e = pool.back();
+        pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void KernelTimer::begin(hipStream_t s, const char* family, hipEvent_t* a) {
+    (void)family;
+    *a = get();
+    if (*a && hipEventRecord(*a, s) != hipSuccess) {
+        pool.push_back(*a);
+        *a = nullptr;
+    }
+}
+
+void KernelTimer::end(hipStream_t s, const char* family, hipEvent_t a) {
+    hipEvent_t b = get();
+    if (!b) {
+        pool.push_back(a);
+        return;
+    }
+    if (hipEventRecord(b, s) != hipSuccess) {
+        pool.push_back(a);
+        pool.push_back(b);
+        return;
+    }
+    pending.push_back(Rec{family, a, b});
+}
+
+void KernelTimer::drain() {
+    for (auto& r : pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+            auto& t = totals[r.family];
+            t.first += ms;
+            t.second += 1;
+        }
+        pool.push_back(r.a);
+        pool.push_back(r.b);
+    }
+    pending.clear();
+}
+
+void KernelTimer::reset() {
+    for (auto& r : pending) {
+        pool.push_back(r.a);
+        pool.push_back(r.b);
+    }
+    pending.clear();
+    totals.clear();
+}
+
+KernelTimer::~KernelTimer() {
+    reset();
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+}

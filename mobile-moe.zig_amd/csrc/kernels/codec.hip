@@ -1,0 +1,201 @@
+// Block codecs on gfx950: bit-exact dequantisation of raw GGUF blocks, the
+// one-time repack into the tile layout, and activation quantisation.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace mmhip {
+
+namespace {
+
+constexpr uint32_t kTypeF32 = 0, kTypeF16 = 1, kTypeQ8_0 = 8, kTypeIq2 = 16;
+
+__constant__ uint64_t c_grid[256] = {
+#include "../iq2xxs_grid.inc"
+};
+
+// Raw GGUF bytes are only 2-byte aligned (34 / 66-byte blocks): read u16s.
+__device__ __forceinline__ uint32_t ld16(const uint8_t* p) {
+    return (uint32_t)*reinterpret_cast<const uint16_t*>(p);
+}
+__device__ __forceinline__ uint32_t ld32u(const uint8_t* p) {
+    return ld16(p) | (ld16(p + 2) << 16);
+}
+
+// Q8_0 (dequant.zig:379-390): one thread per output element.
+__global__ void dequant_q8_0_kernel(const uint8_t* __restrict__ raw, uint64_t n, float* __restrict__ out) {
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint8_t* blk = raw + (i >> 5) * 34;
+    float d = f16_bits_to_f32(ld16(blk));
+    out[i] = d * (float)(int8_t)blk[2 + (i & 31)];
+}
+
+// IQ2_XXS (dequant.zig:316-369): one thread per 8-weight group.
+__global__ void dequant_iq2_kernel(const uint8_t* __restrict__ raw, uint64_t n, float* __restrict__ out) {
+    uint64_t grp = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t base = grp * 8;
+    if (base >= n) return;
+    uint64_t sb = base >> 8;
+    uint32_t ib = (uint32_t)((base >> 5) & 7);
+    uint32_t l = (uint32_t)((base >> 3) & 3);
+    const uint8_t* blk = raw + sb * 66;
+    float d = f16_bits_to_f32(ld16(blk));
+    uint32_t a0 = ld32u(blk + 2 + 8 * ib);
+    uint32_t a1 = ld32u(blk + 2 + 8 * ib + 4);
+    float db = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
+    uint64_t gv = c_grid[(a0 >> (8 * l)) & 0xFFu];
+    uint32_t code = (a1 >> (7 * l)) & 0x7Fu;
+    uint32_t s = code | ((uint32_t)(__popc(code) & 1) << 7);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if (base + j < n) {
+            float mag = (float)((gv >> (8 * j)) & 0xFFu);
+            float sign = ((s >> j) & 1u) ? -1.0f : 1.0f;
+            out[base + j] = db * mag * sign;
+        }
+    }
+}
+
+__global__ void dequant_f16_kernel(const uint16_t* __restrict__ raw, uint64_t n, float* __restrict__ out) {
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = f16_bits_to_f32(raw[i]);
+}
+
+// Raw IQ2_XXS -> tile records (layout in device_common.hpp). One thread per
+// (matrix, row tile, superblock column, lane).
+__global__ void repack_iq2_kernel(const uint8_t* __restrict__ raw, uint64_t rows, uint64_t nsb,
+                                  uint64_t tiles, uint64_t total, uint4* __restrict__ recs,
+                                  uint16_t* __restrict__ dvals) {
+    uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    uint32_t lane = (uint32_t)(gid & 63);
+    uint64_t unit = gid >> 6;
+    uint64_t j = unit % nsb;
+    uint64_t t = (unit / nsb) % tiles;
+    uint64_t mat = unit / (nsb * tiles);
+    uint32_t n = lane & 15, g = lane >> 4;
+    uint64_t row = t * 16 + n;
+    uint32_t w[4] = {0, 0, 0, 0};
+    uint32_t dbits = 0;
+    if (row < rows) {
+        const uint8_t* sb = raw + ((mat * rows + row) * nsb + j) * 66;
+        dbits = ld16(sb);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            uint32_t a0 = ld32u(sb + 2 + 8 * s);
+            uint32_t a1 = ld32u(sb + 2 + 8 * s + 4);
+            uint32_t idx = (a0 >> (8 * g)) & 0xFFu;
+            uint32_t code = (a1 >> (7 * g)) & 0x7Fu;
+            uint32_t ls = a1 >> 28;
+            uint32_t rec = (code & 7u) | ((uint32_t)(__popc(code & 15u) & 1) << 3) | (idx << 4) |
+                           (((code >> 4) & 7u) << 12) | (((ls >> g) & 1u) << 15);
+            w[s >> 1] |= rec << (16 * (s & 1));
+        }
+    }
+    recs[gid] = make_uint4(w[0], w[1], w[2], w[3]);
+    if (g == 0) dvals[unit * 16 + n] = (uint16_t)dbits;
+}
+
+// Raw Q8_0 -> tile records: a unit is two 32-column blocks of 16 rows.
+__global__ void repack_q8_kernel(const uint8_t* __restrict__ raw, uint64_t rows, uint64_t nb,
+                                 uint64_t nu, uint64_t tiles, uint64_t total, uint4* __restrict__ recs,
+                                 uint16_t* __restrict__ dvals) {
+    uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    uint32_t lane = (uint32_t)(gid & 63);
+    uint64_t unit = gid >> 6;
+    uint64_t u = unit % nu;
+    uint64_t t = (unit / nu) % tiles;
+    uint64_t mat = unit / (nu * tiles);
+    uint32_t n = lane & 15, g = lane >> 4;
+    uint64_t row = t * 16 + n;
+    uint32_t w[4] = {0, 0, 0, 0};
+    uint32_t dbits[2] = {0, 0};
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        uint64_t blk = 2 * u + b;
+        if (row < rows && blk < nb) {
+            const uint8_t* src = raw + ((mat * rows + row) * nb + blk) * 34;
+            dbits[b] = ld16(src);
+            const uint8_t* q = src + 2 + 8 * g;
+            w[2 * b] = ld32u(q);
+            w[2 * b + 1] = ld32u(q + 4);
+        }
+    }
+    recs[gid] = make_uint4(w[0], w[1], w[2], w[3]);
+    if (g == 0) {
+        dvals[(unit * 16 + n) * 2] = (uint16_t)dbits[0];
+        dvals[(unit * 16 + n) * 2 + 1] = (uint16_t)dbits[1];
+    }
+}
+
+// One 32-lane group per 32-column block.
+__global__ void quantize_kernel(const float* __restrict__ x, uint64_t x_stride, uint32_t n_vec,
+                                uint32_t cols, uint32_t cols_pad, int8_t* __restrict__ hi,
+                                int8_t* __restrict__ lo, float* __restrict__ sc, uint64_t q_stride,
+                                uint64_t s_stride) {
+    uint32_t nblk = cols_pad / 32;
+    uint64_t blk = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+    uint32_t j = threadIdx.x & 31;
+    if (blk >= (uint64_t)n_vec * nblk) return;  // whole 32-lane group exits together
+    uint64_t v = blk / nblk;
+    uint32_t b = (uint32_t)(blk % nblk);
+    uint32_t col = b * 32 + j;
+    float xv = col < cols ? x[v * x_stride + col] : 0.0f;
+    int8_t h, l;
+    float s = quantize_block32(xv, &h, &l);
+    hi[v * q_stride + col] = h;
+    lo[v * q_stride + col] = l;
+    if (j == 0) sc[v * s_stride + b] = s;
+}
+
+}  // namespace
+
+hipError_t launch_dequant(const void* raw, uint32_t type, uint64_t n, float* out, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const int bs = 256;
+    switch (type) {
+        case kTypeF32:
+            return hipMemcpyAsync(out, raw, n * 4, hipMemcpyDeviceToDevice, s);
+        case kTypeF16:
+            dequant_f16_kernel<<<(unsigned)((n + bs - 1) / bs), bs, 0, s>>>((const uint16_t*)raw, n, out);
+            break;
+        case kTypeQ8_0:
+            dequant_q8_0_kernel<<<(unsigned)((n + bs - 1) / bs), bs, 0, s>>>((const uint8_t*)raw, n, out);
+            break;
+        case kTypeIq2: {
+            uint64_t groups = (n + 7) / 8;
+            dequant_iq2_kernel<<<(unsigned)((groups + bs - 1) / bs), bs, 0, s>>>((const uint8_t*)raw, n, out);
+            break;
+        }
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_repack(const void* raw, const TileGeom& g, uint4* recs, uint16_t* dvals, hipStream_t s) {
+    uint64_t total = g.count * g.tiles * g.units * 64;
+    if (total == 0) return hipSuccess;
+    const int bs = 256;
+    unsigned grid = (unsigned)((total + bs - 1) / bs);
+    if (g.fmt == kFmtIq2) {
+        repack_iq2_kernel<<<grid, bs, 0, s>>>((const uint8_t*)raw, g.rows, g.units, g.tiles, total, recs, dvals);
+    } else {
+        uint64_t nb = (g.cols + 31) / 32;
+        repack_q8_kernel<<<grid, bs, 0, s>>>((const uint8_t*)raw, g.rows, nb, g.units, g.tiles, total, recs, dvals);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize(const float* x, uint64_t x_stride, uint32_t n_vec, uint32_t cols,
+                           uint32_t cols_pad, const QuantAct& q, hipStream_t s) {
+    uint64_t threads = (uint64_t)n_vec * cols_pad;
+    if (threads == 0) return hipSuccess;
+    const int bs = 256;
+    quantize_kernel<<<(unsigned)((threads + bs - 1) / bs), bs, 0, s>>>(
+        x, x_stride, n_vec, cols, cols_pad, q.hi, q.lo, q.scale, q.stride, q.scale_stride);
+    return hipGetLastError();
+}
+
+}  // namespace mmhip

@@ -1,0 +1,676 @@
+/*
+ * CPU oracle: plain-C restatement of the reference algorithm for the
+ * quantized-matrix / MoE-FFN path. TEST INFRASTRUCTURE ONLY (see oracle.h):
+ * loaded by tests, smoke() and bench.py's cpu_baseline leg, never by the HIP
+ * library. Build: oracle/Makefile (-ffp-contract=off).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* Formats                                                              */
+/* ------------------------------------------------------------------ */
+
+static const uint64_t k_grid[256] = {
+#include "../mobile-moe.zig_amd/csrc/iq2xxs_grid.inc"
+};
+
+uint64_t orc_iq2xxs_grid(uint32_t idx) { return k_grid[idx & 255u]; }
+
+/* ksigns_iq2xs (dequant.zig:293-302): the 7-bit sign code with an 8th bit
+ * that makes the total number of negative signs even. */
+uint8_t orc_ksigns(uint32_t code) {
+    code &= 0x7Fu;
+    return (uint8_t)(code | ((uint32_t)__builtin_parity(code) << 7));
+}
+
+static float bits_to_f32(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
+static uint32_t f32_to_bits(float f) { uint32_t b; memcpy(&b, &f, 4); return b; }
+
+/* f16ToF32, dequant.zig:19-47: build the binary32 pattern field by field;
+ * subnormal halves are normalised by shifting the mantissa up (28-36);
+ * Inf/NaN keep the payload (38-42). */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15);
+    uint32_t e = (uint32_t)((h >> 10) & 0x1Fu);
+    uint32_t m = (uint32_t)(h & 0x3FFu);
+    if (e == 0) {
+        if (m == 0) return bits_to_f32(sign << 31);
+        uint32_t shifts = 0;
+        while ((m & 0x400u) == 0) { m <<= 1; ++shifts; }
+        m &= 0x3FFu;
+        return bits_to_f32((sign << 31) | ((113u - shifts) << 23) | (m << 13));
+    }
+    if (e == 31) return bits_to_f32((sign << 31) | 0x7F800000u | (m << 13));
+    return bits_to_f32((sign << 31) | ((e + 112u) << 23) | (m << 13));
+}
+
+/* f32ToF16, dequant.zig:50-95. Normal results round to nearest-even (82-90);
+ * f32 zero/subnormal inputs and results below 2^-24 flush to zero (59-61,
+ * 72-74). Subnormal-result branch (76-77): the reference shifts the 24-bit
+ * significand right by (1 - exp16) instead of (14 - exp16), so the "mantissa"
+ * overflows 10 bits and the final @intCast to u16 traps in safe builds. The
+ * restatement reports that case through *defect (and returns the low 16
+ * bits); nothing on the hot path converts to f16. */
+uint16_t orc_f32_to_f16(float v, int* defect) {
+    uint32_t bits = f32_to_bits(v);
+    uint32_t sign = (bits >> 31) & 1u;
+    uint32_t er = (bits >> 23) & 0xFFu;
+    uint32_t mant = bits & 0x7FFFFFu;
+    uint32_t e = 0, m = 0;
+    if (defect) *defect = 0;
+    if (er == 0) {
+        e = 0; m = 0;
+    } else if (er == 0xFF) {
+        e = 0x1F;
+        m = mant >> 13;
+        if (mant != 0 && m == 0) m = 1;
+    } else {
+        int e16 = (int)er - 127 + 15;
+        if (e16 >= 31) {
+            e = 0x1F; m = 0;
+        } else if (e16 <= 0) {
+            if (e16 < -10) {
+                e = 0; m = 0;
+            } else {
+                e = 0;
+                m = (mant | 0x800000u) >> (uint32_t)(1 - e16);
+                if (defect) *defect = 1;
+            }
+        } else {
+            e = (uint32_t)e16;
+            m = mant >> 13;
+            uint32_t rb = mant & 0x1FFFu;
+            if (rb > 0x1000u || (rb == 0x1000u && (m & 1u))) {
+                ++m;
+                if (m == 0x400u) { m = 0; ++e; }
+            }
+        }
+    }
+    return (uint16_t)((sign << 15) | (e << 10) | m);
+}
+
+/* GgmlType.blockSize / blockBytes / tensorBytes, gguf.zig:59-117 (the types
+ * on this path). */
+uint64_t orc_block_size(uint32_t type) {
+    switch (type) {
+        case ORC_F32: case ORC_F16: return 1;
+        case ORC_Q8_0: return 32;
+        case ORC_IQ2_XXS: return 256;
+        default: return 0;
+    }
+}
+uint64_t orc_block_bytes(uint32_t type) {
+    switch (type) {
+        case ORC_F32: return 4;
+        case ORC_F16: return 2;
+        case ORC_Q8_0: return 34;
+        case ORC_IQ2_XXS: return 66;
+        default: return 0;
+    }
+}
+uint64_t orc_tensor_bytes(uint32_t type, uint64_t n) {
+    uint64_t bs = orc_block_size(type), bb = orc_block_bytes(type);
+    if (bs == 0) return 0;
+    return ((n + bs - 1) / bs) * bb;
+}
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* dequantizeQ8_0, dequant.zig:379-390: block = {f16 d; i8 qs[32]} (34 B);
+ * out[32 i + j] = f16ToF32(d) * qs[j]. */
+void orc_dequantize_q8_0(const uint8_t* data, uint64_t n, float* out) {
+    uint64_t nb = (n + 31) / 32;
+    for (uint64_t b = 0; b < nb; ++b) {
+        const uint8_t* blk = data + b * 34;
+        float d = orc_f16_to_f32(rd16(blk));
+        for (uint64_t j = 0; j < 32 && b * 32 + j < n; ++j)
+            out[b * 32 + j] = d * (float)(int8_t)blk[2 + j];
+    }
+}
+
+/* dequantizeBlock, dequant.zig:316-354. 256 weights in 8 groups of 32; group
+ * ib uses qs[4ib..4ib+3]: the first u32 holds four grid indices (byte l), the
+ * second holds four 7-bit sign codes (bits 7l..7l+6) and a 4-bit scale in
+ * bits 28..31. w = (d * (0.5 + ls) * 0.25) * grid_byte * sign. */
+void orc_dequantize_iq2xxs_block(const uint8_t* blk, float* out) {
+    float d = orc_f16_to_f32(rd16(blk));
+    const uint8_t* qs = blk + 2;
+    for (int ib = 0; ib < 8; ++ib) {
+        uint32_t a0 = (uint32_t)rd16(qs + 8 * ib) | ((uint32_t)rd16(qs + 8 * ib + 2) << 16);
+        uint32_t a1 = (uint32_t)rd16(qs + 8 * ib + 4) | ((uint32_t)rd16(qs + 8 * ib + 6) << 16);
+        float ls = (float)(a1 >> 28);
+        float db = d * (0.5f + ls) * 0.25f;
+        for (int l = 0; l < 4; ++l) {
+            uint32_t gi = (a0 >> (8 * l)) & 0xFFu;
+            uint64_t g = k_grid[gi];
+            uint8_t s = orc_ksigns((a1 >> (7 * l)) & 0x7Fu);
+            for (int j = 0; j < 8; ++j) {
+                float sign = ((s >> j) & 1u) ? -1.0f : 1.0f;
+                float mag = (float)((g >> (8 * j)) & 0xFFu);
+                out[ib * 32 + l * 8 + j] = db * mag * sign;
+            }
+        }
+    }
+}
+
+/* dequantizeIQ2XXS, dequant.zig:358-369. */
+void orc_dequantize_iq2xxs(const uint8_t* data, uint64_t n, float* out) {
+    uint64_t nb = (n + 255) / 256;
+    float tmp[256];
+    for (uint64_t b = 0; b < nb; ++b) {
+        orc_dequantize_iq2xxs_block(data + b * 66, tmp);
+        uint64_t cnt = (n - b * 256) < 256 ? (n - b * 256) : 256;
+        memcpy(out + b * 256, tmp, cnt * sizeof(float));
+    }
+}
+
+/* dequantize dispatch, dequant.zig:632-659 (types on this path). */
+int orc_dequantize(const uint8_t* data, uint32_t type, uint64_t n, float* out) {
+    switch (type) {
+        case ORC_F32: memcpy(out, data, n * 4); return 0;
+        case ORC_F16:
+            for (uint64_t i = 0; i < n; ++i) out[i] = orc_f16_to_f32(rd16(data + 2 * i));
+            return 0;
+        case ORC_Q8_0: orc_dequantize_q8_0(data, n, out); return 0;
+        case ORC_IQ2_XXS: orc_dequantize_iq2xxs(data, n, out); return 0;
+        default: return -1;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* CPU kernels                                                          */
+/* ------------------------------------------------------------------ */
+
+/* @reduce(.Add) over @Vector(4, f32), strict mode: ordered lane sum. */
+static float reduce4(const float v[4]) { return ((v[0] + v[1]) + v[2]) + v[3]; }
+
+/* matVecMulQ8_0, qmm.zig:13-50: one 4-lane accumulator per row, lane =
+ * column mod 4; per-block tail goes to lane 0; row result = @reduce. */
+void orc_matvec_q8_0(float* out, const uint8_t* blocks, const float* x,
+                     size_t out_dim, size_t in_dim) {
+    size_t bpr = (in_dim + 31) / 32;
+    for (size_t row = 0; row < out_dim; ++row) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        size_t col = 0;
+        for (size_t b = 0; b < bpr; ++b) {
+            const uint8_t* blk = blocks + (row * bpr + b) * 34;
+            const int8_t* q = (const int8_t*)(blk + 2);
+            float d = orc_f16_to_f32(rd16(blk));
+            size_t qi = 0;
+            for (; qi + 4 <= 32 && col + 4 <= in_dim; qi += 4, col += 4) {
+                for (int l = 0; l < 4; ++l) {
+                    float w = d * (float)q[qi + l];
+                    acc[l] = acc[l] + w * x[col + l];
+                }
+            }
+            for (; qi < 32 && col < in_dim; ++qi, ++col) {
+                float w = d * (float)q[qi];
+                acc[0] = acc[0] + w * x[col];
+            }
+        }
+        out[row] = reduce4(acc);
+    }
+}
+
+/* matMulQ8_0, qmm.zig:58-138: C[m, n] (row-major, out[mi * n + ni]) =
+ * A_q8[m, k] . B[n, k]^T; 64x64 blocking; per 4-weight group and per column,
+ * out += @reduce(w_vec * b_vec); per-block scalar tail. */
+void orc_matmul_q8_0(float* out, const uint8_t* a, const float* b,
+                     size_t m, size_t n, size_t k) {
+    size_t bpr = (k + 31) / 32;
+    memset(out, 0, m * n * sizeof(float));
+    const size_t MB = 64, NB = 64;
+    for (size_t mi = 0; mi < m; mi += MB) {
+        size_t m_end = mi + MB < m ? mi + MB : m;
+        for (size_t ni = 0; ni < n; ni += NB) {
+            size_t n_end = ni + NB < n ? ni + NB : n;
+            for (size_t r = mi; r < m_end; ++r) {
+                size_t col = 0;
+                for (size_t bi = 0; bi < bpr; ++bi) {
+                    const uint8_t* blk = a + (r * bpr + bi) * 34;
+                    const int8_t* q = (const int8_t*)(blk + 2);
+                    float d = orc_f16_to_f32(rd16(blk));
+                    size_t qi = 0;
+                    for (; qi + 4 <= 32 && col + 4 <= k; qi += 4, col += 4) {
+                        float w[4];
+                        for (int l = 0; l < 4; ++l) w[l] = d * (float)q[qi + l];
+                        for (size_t c = ni; c < n_end; ++c) {
+                            const float* br = b + c * k + col;
+                            float p[4];
+                            for (int l = 0; l < 4; ++l) p[l] = w[l] * br[l];
+                            out[r * n + c] = out[r * n + c] + reduce4(p);
+                        }
+                    }
+                    for (; qi < 32 && col < k; ++qi, ++col) {
+                        float w = d * (float)q[qi];
+                        for (size_t c = ni; c < n_end; ++c)
+                            out[r * n + c] = out[r * n + c] + w * b[c * k + col];
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* math.matVecMul, math.zig:79-99: 4-lane accumulator, @reduce, scalar tail. */
+void orc_matvec_f32(float* out, const float* w, const float* x,
+                    size_t out_dim, size_t in_dim) {
+    for (size_t row = 0; row < out_dim; ++row) {
+        const float* wr = w + row * in_dim;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        size_t j = 0;
+        for (; j + 4 <= in_dim; j += 4)
+            for (int l = 0; l < 4; ++l) acc[l] = acc[l] + wr[j + l] * x[j + l];
+        float s = reduce4(acc);
+        for (; j < in_dim; ++j) s = s + wr[j] * x[j];
+        out[row] = s;
+    }
+}
+
+/* math.dot, math.zig:59-74. */
+float orc_dot(const float* a, const float* b, size_t n) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    size_t i = 0;
+    for (; i + 4 <= n; i += 4)
+        for (int l = 0; l < 4; ++l) acc[l] = acc[l] + a[i + l] * b[i + l];
+    float s = reduce4(acc);
+    for (; i < n; ++i) s = s + a[i] * b[i];
+    return s;
+}
+
+/* math.silu / siluInplace / mul, math.zig:38-54. */
+float orc_silu(float x) { return x / (1.0f + expf(-x)); }
+void orc_silu_inplace(float* x, size_t n) { for (size_t i = 0; i < n; ++i) x[i] = orc_silu(x[i]); }
+void orc_mul(float* out, const float* a, const float* b, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = a[i] * b[i];
+}
+
+/* siftDownMin, math.zig:177-193. */
+static void sift_down_min(uint32_t* hi, float* hs, size_t start, size_t end) {
+    size_t parent = start;
+    for (;;) {
+        size_t left = parent * 2 + 1, right = left + 1, smallest = parent;
+        if (left < end && hs[left] < hs[smallest]) smallest = left;
+        if (right < end && hs[right] < hs[smallest]) smallest = right;
+        if (smallest == parent) break;
+        uint32_t ti = hi[parent]; hi[parent] = hi[smallest]; hi[smallest] = ti;
+        float ts = hs[parent]; hs[parent] = hs[smallest]; hs[smallest] = ts;
+        parent = smallest;
+    }
+}
+
+/* topK, math.zig:130-174: size-k min-heap seeded with the first k scores,
+ * later scores replace the root only when strictly greater; results are
+ * popped from the root into result[k-1], result[k-2], ... (descending). */
+size_t orc_topk(const float* scores, size_t n, size_t k, uint32_t* idx_out,
+                float* score_out) {
+    if (k == 0 || k > n) return 0;
+    uint32_t hi[64];
+    float hs[64];
+    if (k > 64) return 0;
+    for (size_t i = 0; i < k; ++i) { hi[i] = (uint32_t)i; hs[i] = scores[i]; }
+    for (size_t i = k / 2; i > 0;) { --i; sift_down_min(hi, hs, i, k); }
+    for (size_t j = k; j < n; ++j) {
+        if (scores[j] > hs[0]) {
+            hi[0] = (uint32_t)j; hs[0] = scores[j];
+            sift_down_min(hi, hs, 0, k);
+        }
+    }
+    for (size_t ri = k; ri > 0;) {
+        --ri;
+        idx_out[ri] = hi[0]; score_out[ri] = hs[0];
+        hi[0] = hi[ri]; hs[0] = hs[ri];
+        sift_down_min(hi, hs, 0, ri);
+    }
+    return k;
+}
+
+/* ------------------------------------------------------------------ */
+/* Engine seam, CPU branch (inference.zig:1200-1264)                     */
+/* ------------------------------------------------------------------ */
+
+int orc_mat_vec_mul_unified(float* out, const uint8_t* ptr, uint32_t type,
+                            const float* x, size_t out_dim, size_t in_dim) {
+    if (type == ORC_Q8_0) {
+        orc_matvec_q8_0(out, ptr, x, out_dim, in_dim);
+        return 0;
+    }
+    /* else-branch: dequantize the whole matrix into a fresh f32 buffer, then
+     * math.matVecMul (1222-1226). */
+    float* w = (float*)malloc(out_dim * in_dim * sizeof(float));
+    if (!w) return -2;
+    if (orc_dequantize(ptr, type, (uint64_t)out_dim * in_dim, w) != 0) { free(w); return -1; }
+    orc_matvec_f32(out, w, x, out_dim, in_dim);
+    free(w);
+    return 0;
+}
+
+int orc_batch_mat_mul_unified(float* out, const uint8_t* ptr, uint32_t type,
+                              const float* in, size_t out_dim, size_t batch,
+                              size_t in_dim) {
+    if (type == ORC_Q8_0) {
+        float* tmp = (float*)malloc(out_dim * batch * sizeof(float));
+        if (!tmp) return -2;
+        orc_matmul_q8_0(tmp, ptr, in, out_dim, batch, in_dim);
+        for (size_t bi = 0; bi < batch; ++bi)       /* transpose, 1250-1254 */
+            for (size_t oi = 0; oi < out_dim; ++oi)
+                out[bi * out_dim + oi] = tmp[oi * batch + bi];
+        free(tmp);
+        return 0;
+    }
+    float* w = (float*)malloc(out_dim * in_dim * sizeof(float));
+    if (!w) return -2;
+    if (orc_dequantize(ptr, type, (uint64_t)out_dim * in_dim, w) != 0) { free(w); return -1; }
+    for (size_t bi = 0; bi < batch; ++bi)
+        orc_matvec_f32(out + bi * out_dim, w, in + bi * in_dim, out_dim, in_dim);
+    free(w);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Routing                                                              */
+/* ------------------------------------------------------------------ */
+
+/* ThrottleState.throttle, thermal.zig:44-72 (fields used by routing). */
+void orc_throttle_set(orc_throttle* t, int level) {
+    static const uint32_t limit[4] = {4, 3, 2, 1};
+    static const int hot_cpu[4] = {0, 0, 1, 1};
+    if (level < 0 || level > 3) level = 0;
+    t->level = level;
+    t->active_expert_limit = limit[level];
+    t->hot_experts_on_cpu = hot_cpu[level];
+}
+
+/* getRoutedScalingFactor, scheduler.zig:254-262. */
+static float routed_scale(const orc_throttle* t, float rsf) {
+    switch (t->level) {
+        case ORC_LIGHT: return rsf * 0.83f;
+        case ORC_MEDIUM: return rsf * 0.67f;
+        case ORC_HEAVY: return rsf * 0.5f;
+        default: return rsf;
+    }
+}
+
+static int cmp_desc_u64(const void* a, const void* b) {
+    uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return x < y ? 1 : (x > y ? -1 : 0);
+}
+
+/* ExpertStats.isHot / hotThreshold, scheduler.zig:46-75 (n_experts <= 256). */
+static int expert_is_hot(const orc_expert_stats* s, uint32_t layer, uint32_t eid) {
+    if (!s) return 0;
+    uint64_t thr = 0;
+    if (s->total_tokens != 0) {
+        uint64_t buf[256];
+        uint32_t n = s->n_experts;
+        memcpy(buf, s->counts + (size_t)layer * n, n * sizeof(uint64_t));
+        qsort(buf, n, sizeof(uint64_t), cmp_desc_u64);
+        uint32_t k = n / 5 > 1 ? n / 5 : 1;
+        thr = buf[k - 1];
+    }
+    return s->counts[(size_t)layer * s->n_experts + eid] >= thr;
+}
+
+/* Scheduler.route, scheduler.zig:169-252. */
+uint32_t orc_route(orc_expert_stats* stats, uint32_t layer,
+                   const orc_throttle* thr, float rsf,
+                   const float* scores, uint32_t n_experts,
+                   uint32_t* ids, float* w, int* targets, int* deferred) {
+    uint32_t k = thr->active_expert_limit < 4 ? thr->active_expert_limit : 4;
+    float ts[4];
+    if (k == 0 || orc_topk(scores, n_experts, k, ids, ts) != k) return 0;
+    float mx = ts[0];
+    for (uint32_t i = 1; i < k; ++i) if (ts[i] > mx) mx = ts[i];
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < k; ++i) { w[i] = expf(ts[i] - mx); sum = sum + w[i]; }
+    for (uint32_t i = 0; i < k; ++i) w[i] = w[i] / sum;
+    for (uint32_t i = 0; i < k; ++i) w[i] = w[i] * routed_scale(thr, rsf);
+    int hot[4];
+    for (uint32_t i = 0; i < k; ++i) {
+        hot[i] = expert_is_hot(stats, layer, ids[i]);
+        targets[i] = hot[i] ? ORC_TARGET_GPU : ORC_TARGET_CPU;
+        if (hot[i] && thr->hot_experts_on_cpu) targets[i] = ORC_TARGET_CPU;
+    }
+    if (stats)
+        for (uint32_t i = 0; i < k; ++i) stats->counts[(size_t)layer * stats->n_experts + ids[i]] += 1;
+    *deferred = 0;
+    if (thr->level == ORC_HEAVY && k > 1) {
+        for (uint32_t i = 1; i < k; ++i) { targets[i] = ORC_TARGET_SKIPPED; *deferred = 1; }
+        float rem = 0.0f;
+        for (uint32_t i = 0; i < k; ++i) if (targets[i] != ORC_TARGET_SKIPPED) rem = rem + w[i];
+        if (rem > 0.0f) {
+            float scale = routed_scale(thr, rsf) / rem;
+            for (uint32_t i = 0; i < k; ++i) if (targets[i] != ORC_TARGET_SKIPPED) w[i] = w[i] * scale;
+        }
+    }
+    if (stats) stats->total_tokens += 1;
+    return k;
+}
+
+/* ------------------------------------------------------------------ */
+/* Thread pool (thread_pool.zig:15-99): fixed workers, FIFO queue under a   */
+/* mutex + condition variable, waitAll until queue empty and none running. */
+/* ------------------------------------------------------------------ */
+
+typedef struct { void (*fn)(void*); void* ctx; } orc_task;
+
+struct orc_pool {
+    pthread_t* threads;
+    int n;
+    orc_task q[64];
+    int head, count, running, shutdown;
+    pthread_mutex_t mu;
+    pthread_cond_t cv;
+};
+
+static void* pool_worker(void* arg) {
+    orc_pool* p = (orc_pool*)arg;
+    for (;;) {
+        pthread_mutex_lock(&p->mu);
+        while (p->count == 0 && !p->shutdown) pthread_cond_wait(&p->cv, &p->mu);
+        if (p->shutdown && p->count == 0) { pthread_mutex_unlock(&p->mu); break; }
+        orc_task t = p->q[p->head];
+        p->head = (p->head + 1) % 64;
+        p->count--;
+        p->running++;
+        pthread_mutex_unlock(&p->mu);
+        t.fn(t.ctx);
+        pthread_mutex_lock(&p->mu);
+        p->running--;
+        pthread_cond_broadcast(&p->cv);
+        pthread_mutex_unlock(&p->mu);
+    }
+    return NULL;
+}
+
+orc_pool* orc_pool_create(int n) {
+    orc_pool* p = (orc_pool*)calloc(1, sizeof(orc_pool));
+    if (!p) return NULL;
+    p->threads = (pthread_t*)calloc((size_t)n, sizeof(pthread_t));
+    p->n = n;
+    pthread_mutex_init(&p->mu, NULL);
+    pthread_cond_init(&p->cv, NULL);
+    for (int i = 0; i < n; ++i) pthread_create(&p->threads[i], NULL, pool_worker, p);
+    return p;
+}
+
+void orc_pool_destroy(orc_pool* p) {
+    if (!p) return;
+    pthread_mutex_lock(&p->mu);
+    p->shutdown = 1;
+    pthread_cond_broadcast(&p->cv);
+    pthread_mutex_unlock(&p->mu);
+    for (int i = 0; i < p->n; ++i) pthread_join(p->threads[i], NULL);
+    pthread_mutex_destroy(&p->mu);
+    pthread_cond_destroy(&p->cv);
+    free(p->threads);
+    free(p);
+}
+
+static void pool_submit(orc_pool* p, void (*fn)(void*), void* ctx) {
+    if (!p) { fn(ctx); return; }
+    pthread_mutex_lock(&p->mu);
+    p->q[(p->head + p->count) % 64] = (orc_task){fn, ctx};
+    p->count++;
+    pthread_cond_broadcast(&p->cv);
+    pthread_mutex_unlock(&p->mu);
+}
+
+static void pool_wait_all(orc_pool* p) {
+    if (!p) return;
+    pthread_mutex_lock(&p->mu);
+    while (p->count > 0 || p->running > 0) pthread_cond_wait(&p->cv, &p->mu);
+    pthread_mutex_unlock(&p->mu);
+}
+
+/* ------------------------------------------------------------------ */
+/* MoE FFN (inference.zig:886-1188)                                      */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    float* out;
+    const uint8_t* ptr;
+    uint32_t type;
+    const float* in;
+    size_t out_dim, in_dim;
+    int err;
+} matvec_task;
+
+static void matvec_task_run(void* c) {       /* MatVecTask.run, 1023-1028 */
+    matvec_task* t = (matvec_task*)c;
+    t->err = orc_mat_vec_mul_unified(t->out, t->ptr, t->type, t->in, t->out_dim, t->in_dim);
+}
+
+/* expertFFN, inference.zig:1152-1188. */
+static int expert_ffn(const orc_moe_desc* d, uint32_t eid, const float* h, float* result) {
+    size_t inter = d->moe_inter, hid = d->hidden;
+    uint64_t gu_bytes = orc_tensor_bytes(d->expert_type, (uint64_t)inter * hid);
+    uint64_t dn_bytes = orc_tensor_bytes(d->expert_type, (uint64_t)hid * inter);
+    float* g = (float*)malloc(inter * sizeof(float));
+    float* u = (float*)malloc(inter * sizeof(float));
+    int rc = -2;
+    if (g && u) {
+        rc = orc_mat_vec_mul_unified(g, d->expert_gate + eid * gu_bytes, d->expert_type, h, inter, hid);
+        if (!rc) rc = orc_mat_vec_mul_unified(u, d->expert_up + eid * gu_bytes, d->expert_type, h, inter, hid);
+        if (!rc) {
+            orc_silu_inplace(g, inter);
+            orc_mul(u, g, u, inter);
+            rc = orc_mat_vec_mul_unified(result, d->expert_down + eid * dn_bytes, d->expert_type, u, hid, inter);
+        }
+    }
+    free(g);
+    free(u);
+    return rc;
+}
+
+typedef struct {
+    const orc_moe_desc* d;
+    uint32_t eid;
+    const float* h;
+    float* out;
+    int err;
+} expert_task;
+
+static void expert_task_run(void* c) {       /* ExpertTask.run, 941-949 */
+    expert_task* t = (expert_task*)c;
+    t->err = expert_ffn(t->d, t->eid, t->h, t->out);
+}
+
+/* sharedExpertFFN, inference.zig:1094-1146: gate/up as two pool tasks,
+ * down on the caller. */
+static int shared_expert_ffn(const orc_moe_desc* d, orc_pool* pool, const float* h, float* result) {
+    size_t inter = d->shared_inter, hid = d->hidden;
+    float* g = (float*)malloc(inter * sizeof(float));
+    float* u = (float*)malloc(inter * sizeof(float));
+    int rc = -2;
+    if (g && u) {
+        matvec_task tg = {g, d->shared_gate, d->shared_type, h, inter, hid, 0};
+        matvec_task tu = {u, d->shared_up, d->shared_type, h, inter, hid, 0};
+        pool_submit(pool, matvec_task_run, &tg);
+        pool_submit(pool, matvec_task_run, &tu);
+        pool_wait_all(pool);
+        rc = tg.err ? tg.err : tu.err;
+        if (!rc) {
+            orc_silu_inplace(g, inter);
+            orc_mul(u, g, u, inter);
+            rc = orc_mat_vec_mul_unified(result, d->shared_down, d->shared_type, u, hid, inter);
+        }
+    }
+    free(g);
+    free(u);
+    return rc;
+}
+
+/* moeFFN, inference.zig:886-1010 (MoE branch; the leading dense layers are
+ * not on this path). */
+int orc_moe_ffn(const orc_moe_desc* d, orc_pool* pool, orc_expert_stats* stats,
+                uint32_t layer, const orc_throttle* thr, const float* hidden_in,
+                float* hidden_out, uint32_t* route_ids, float* route_w) {
+    size_t hid = d->hidden;
+    float* scores = (float*)malloc(d->n_experts * sizeof(float));
+    if (!scores) return -2;
+    int rc = orc_mat_vec_mul_unified(scores, d->router, d->router_type, hidden_in, d->n_experts, hid);
+    if (rc) { free(scores); return rc; }
+    uint32_t ids[4];
+    float w[4];
+    int targets[4], deferred = 0;
+    uint32_t k = orc_route(stats, layer, thr, d->routed_scaling_factor, scores, d->n_experts,
+                           ids, w, targets, &deferred);
+    free(scores);
+    if (k == 0) return -3;
+    float* ffn = (float*)calloc(hid, sizeof(float));
+    float* eo[4] = {0, 0, 0, 0};
+    expert_task tasks[4];
+    uint32_t active = 0;
+    for (uint32_t i = 0; i < k; ++i) if (targets[i] != ORC_TARGET_SKIPPED) ++active;
+    for (uint32_t i = 0; i < active; ++i) eo[i] = (float*)calloc(hid, sizeof(float));
+    uint32_t oi = 0;
+    for (uint32_t i = 0; i < k; ++i) {
+        if (targets[i] == ORC_TARGET_SKIPPED) continue;
+        tasks[oi] = (expert_task){d, ids[i], hidden_in, eo[oi], 0};
+        pool_submit(pool, expert_task_run, &tasks[oi]);
+        ++oi;
+    }
+    pool_wait_all(pool);
+    for (uint32_t i = 0; i < oi; ++i) if (tasks[i].err) rc = tasks[i].err;
+    if (!rc) {
+        oi = 0;                                   /* weighted sum, 977-986 */
+        for (uint32_t i = 0; i < k; ++i) {
+            if (targets[i] == ORC_TARGET_SKIPPED) continue;
+            for (size_t j = 0; j < hid; ++j) ffn[j] = ffn[j] + w[i] * eo[oi][j];
+            ++oi;
+        }
+        if (d->shared_gate) {                     /* shared expert, 990-997 */
+            float* s = (float*)malloc(hid * sizeof(float));
+            rc = shared_expert_ffn(d, pool, hidden_in, s);
+            if (!rc) for (size_t j = 0; j < hid; ++j) ffn[j] = ffn[j] + s[j];
+            free(s);
+        }
+        if (!rc && deferred && d->deferral_bias)  /* 1000-1006 */
+            for (size_t j = 0; j < hid; ++j) ffn[j] = ffn[j] + d->deferral_bias[j];
+        if (!rc) memcpy(hidden_out, ffn, hid * sizeof(float));
+    }
+    for (uint32_t i = 0; i < active; ++i) free(eo[i]);
+    free(ffn);
+    if (route_ids) for (uint32_t i = 0; i < k; ++i) route_ids[i] = ids[i];
+    if (route_w) for (uint32_t i = 0; i < k; ++i) route_w[i] = w[i];
+    return rc ? rc : (int)k;
+}
+
+int orc_moe_ffn_batch(const orc_moe_desc* d, orc_pool* pool, orc_expert_stats* stats,
+                      uint32_t layer, const orc_throttle* thr, const float* hidden_in,
+                      float* hidden_out, uint32_t n_tokens, uint32_t* route_ids, float* route_w) {
+    int k = 0;
+    for (uint32_t t = 0; t < n_tokens; ++t) {
+        k = orc_moe_ffn(d, pool, stats, layer, thr, hidden_in + (size_t)t * d->hidden,
+                        hidden_out + (size_t)t * d->hidden,
+                        route_ids ? route_ids + 4 * t : NULL, route_w ? route_w + 4 * t : NULL);
+        if (k < 0) return k;
+    }
+    return k;
+}

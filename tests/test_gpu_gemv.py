@@ -1,0 +1,217 @@
+"""GPU parity of the decode GEMV and batched QMM against the oracle
+(qmm.zig:13-138, math.zig:79-99, inference.zig:1200-1264). Tolerance:
+max|y - ref| / max|ref| <= 1e-3 for the f32-accumulating GEMV paths and
+1e-2 for the MFMA QMM path (the path's stated bars); the 16-bit block
+fixed-point activations keep both far below that (~2e-5)."""
+import threading
+
+import numpy as np
+import pytest
+
+import mmhip as mm
+
+pytestmark = pytest.mark.gpu
+
+TOL_GEMV = 1e-3
+TOL_QMM = 1e-2
+
+
+def _weights(rng, t, rows, cols, count=1):
+    return mm.make_weight(rng, t, rows, cols, count)
+
+
+@pytest.mark.parametrize("t", [mm.Q8_0, mm.IQ2_XXS])
+@pytest.mark.parametrize("rows,cols", [(1536, 2048), (2048, 1536)])
+def test_gemv_config_shapes(ctx, orc, t, rows, cols):
+    rng = np.random.default_rng(rows * 3 + t)
+    raw = _weights(rng, t, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    ref = orc.mat_vec_mul_unified(raw, t, x, rows, cols)
+    got = ctx.mat_vec_mul(raw, t, x, rows, cols)
+    err = mm.max_abs_rel(got, ref)
+    print(f"type={t} {rows}x{cols} max_abs_rel={err:.3e}")
+    assert err <= TOL_GEMV
+
+
+@pytest.mark.parametrize("t", [mm.F32, mm.F16])
+def test_gemv_float_router_shape(ctx, orc, t):
+    rng = np.random.default_rng(40 + t)
+    raw = _weights(rng, t, 64, 2048)
+    x = rng.standard_normal(2048).astype(np.float32)
+    ref = orc.mat_vec_mul_unified(raw, t, x, 64, 2048)
+    assert mm.max_abs_rel(ctx.mat_vec_mul(raw, t, x, 64, 2048), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("t,rows,cols", [
+    (mm.Q8_0, 1, 32), (mm.Q8_0, 17, 96), (mm.Q8_0, 33, 40), (mm.Q8_0, 5, 1000),
+    (mm.IQ2_XXS, 1, 256), (mm.IQ2_XXS, 17, 512), (mm.IQ2_XXS, 100, 768),
+    (mm.F32, 3, 5), (mm.F16, 7, 33),
+])
+def test_gemv_ragged_shapes(ctx, orc, t, rows, cols):
+    """Rows not a multiple of the 16-row tile; Q8_0 columns with a partial
+    last block (the reference ignores columns >= in_dim)."""
+    rng = np.random.default_rng(rows * 7 + cols)
+    raw = _weights(rng, t, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    ref = orc.mat_vec_mul_unified(raw, t, x, rows, cols)
+    assert mm.max_abs_rel(ctx.mat_vec_mul(raw, t, x, rows, cols), ref) <= TOL_GEMV
+
+
+def test_gemv_reference_kat_all_ones(ctx, orc):
+    # qmm.zig:213-238 on the device: 4x64 all-127 blocks, d=f16(1/127), x=1 -> 64
+    d, _ = orc.f32_to_f16(1.0 / 127.0)
+    b = np.zeros((8, 34), np.uint8)
+    b[:, 0:2] = np.array([d], np.uint16).view(np.uint8)
+    b[:, 2:] = 127
+    out = ctx.mat_vec_mul(b.reshape(-1), mm.Q8_0, np.ones(64, np.float32), 4, 64)
+    assert np.all(np.abs(out - 64.0) <= 0.1)
+
+
+def test_gemv_structured_layout_probe(ctx, orc):
+    """One-hot activations select single columns: any mistake in the tile
+    layout, the MFMA operand layout or the digit split shows up as a wrong
+    column landing in a row."""
+    rng = np.random.default_rng(77)
+    rows, cols = 48, 512
+    raw = _weights(rng, mm.IQ2_XXS, rows, cols)
+    w = orc.dequantize(raw, orc.IQ2_XXS, rows * cols).reshape(rows, cols)
+    for c in [0, 1, 7, 8, 31, 32, 100, 255, 256, 511]:
+        x = np.zeros(cols, np.float32)
+        x[c] = 1.0
+        got = ctx.mat_vec_mul(raw, mm.IQ2_XXS, x, rows, cols)
+        assert np.allclose(got, w[:, c], rtol=1e-4, atol=1e-7), f"column {c}"
+    rawq = _weights(rng, mm.Q8_0, rows, cols)
+    wq = orc.dequantize(rawq, orc.Q8_0, rows * cols).reshape(rows, cols)
+    for c in [0, 5, 31, 32, 63, 64, 511]:
+        x = np.zeros(cols, np.float32)
+        x[c] = -2.5
+        got = ctx.mat_vec_mul(rawq, mm.Q8_0, x, rows, cols)
+        assert np.allclose(got, -2.5 * wq[:, c], rtol=1e-4, atol=1e-7), f"column {c}"
+
+
+def test_gemv_batched_many_experts_one_launch(ctx, orc):
+    """64 stacked expert matrices in one launch, distinct input per matrix."""
+    rng = np.random.default_rng(8)
+    rows, cols, E = 1536, 2048, 8
+    raw = _weights(rng, mm.IQ2_XXS, rows, cols, E)
+    w = ctx.upload(raw, mm.IQ2_XXS, rows, cols, E)
+    x = rng.standard_normal((E, cols)).astype(np.float32)
+    dx = mm.DeviceArray.from_numpy(ctx, x)
+    dy = mm.DeviceArray(ctx, E * rows * 4)
+    ctx.gemv_batched_dev(w, 0, E, dx, cols, dy, rows)
+    ctx.synchronize()
+    y = dy.to_numpy(np.float32, E * rows).reshape(E, rows)
+    per = mm.tensor_bytes(mm.IQ2_XXS, rows, cols)
+    for e in range(E):
+        ref = orc.mat_vec_mul_unified(raw[e * per:(e + 1) * per], orc.IQ2_XXS, x[e], rows, cols)
+        assert mm.max_abs_rel(y[e], ref) <= TOL_GEMV, f"expert {e}"
+    # shared input vector (x_stride 0), sub-range of matrices
+    ctx.gemv_batched_dev(w, 2, 3, dx, 0, dy, rows)
+    ctx.synchronize()
+    y = dy.to_numpy(np.float32, 3 * rows).reshape(3, rows)
+    for i, e in enumerate(range(2, 5)):
+        ref = orc.mat_vec_mul_unified(raw[e * per:(e + 1) * per], orc.IQ2_XXS, x[0], rows, cols)
+        assert mm.max_abs_rel(y[i], ref) <= TOL_GEMV
+    w.free()
+    dx.free()
+    dy.free()
+
+
+def test_gemv_edge_values(ctx, orc):
+    """Zero input, zero scales, huge and tiny activations, NaN/Inf poisoning."""
+    rng = np.random.default_rng(9)
+    rows, cols = 32, 512
+    raw = _weights(rng, mm.IQ2_XXS, rows, cols)
+    assert np.all(ctx.mat_vec_mul(raw, mm.IQ2_XXS, np.zeros(cols, np.float32), rows, cols) == 0.0)
+    for scale in [1e30, 1e-30]:
+        x = (rng.standard_normal(cols) * scale).astype(np.float32)
+        ref = orc.mat_vec_mul_unified(raw, orc.IQ2_XXS, x, rows, cols)
+        assert mm.max_abs_rel(ctx.mat_vec_mul(raw, mm.IQ2_XXS, x, rows, cols), ref) <= TOL_GEMV
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[3] = np.inf
+    got = ctx.mat_vec_mul(raw, mm.IQ2_XXS, x, rows, cols)
+    ref = orc.mat_vec_mul_unified(raw, orc.IQ2_XXS, x, rows, cols)
+    assert np.all(~np.isfinite(ref)) and np.all(~np.isfinite(got))
+    zero_d = raw.reshape(-1, 66).copy()
+    zero_d[:, 0:2] = 0
+    assert np.all(ctx.mat_vec_mul(zero_d.reshape(-1), mm.IQ2_XXS, np.ones(cols, np.float32), rows, cols) == 0.0)
+
+
+@pytest.mark.parametrize("t", [mm.Q8_0, mm.IQ2_XXS])
+@pytest.mark.parametrize("rows,cols", [(1536, 2048), (2048, 1536)])
+def test_qmm_batch64_config(ctx, orc, t, rows, cols):
+    """Batched prefill QMM, batch 64, against the oracle's batchMatMulUnified."""
+    rng = np.random.default_rng(rows + 5 * t)
+    raw = _weights(rng, t, rows, cols)
+    xin = rng.standard_normal((64, cols)).astype(np.float32)
+    ref = orc.batch_mat_mul_unified(raw, t, xin, rows, 64, cols)
+    got = ctx.batch_mat_mul(raw, t, xin, rows, 64, cols)
+    err = mm.max_abs_rel(got, ref)
+    print(f"qmm type={t} {rows}x{cols} max_abs_rel={err:.3e}")
+    assert err <= TOL_QMM
+    assert err <= TOL_GEMV   # the int8-digit MFMA path also meets the f32 bar
+
+
+@pytest.mark.parametrize("batch", [1, 2, 7, 33, 100])
+def test_qmm_ragged_batches_and_layouts(ctx, orc, batch):
+    rng = np.random.default_rng(batch)
+    rows, cols = 80, 320
+    raw = _weights(rng, mm.Q8_0, rows, cols)
+    xin = rng.standard_normal((batch, cols)).astype(np.float32)
+    ref_mn = orc.matmul_q8_0(raw, xin, rows, batch, cols)          # [rows][batch], qmm.zig layout
+    w = ctx.upload(raw, mm.Q8_0, rows, cols)
+    dx = mm.DeviceArray.from_numpy(ctx, xin)
+    dy = mm.DeviceArray(ctx, rows * batch * 4)
+    for layout in (0, 1):
+        ctx.qmm_dev(w, 0, dx, dy, batch, layout)
+        ctx.synchronize()
+        y = dy.to_numpy(np.float32, rows * batch)
+        y = y.reshape(batch, rows).T if layout == 0 else y.reshape(rows, batch)
+        assert mm.max_abs_rel(y, ref_mn) <= TOL_QMM
+    w.free()
+    dx.free()
+    dy.free()
+
+
+def test_qmm_reference_kats(ctx, orc):
+    # qmm.zig:142-173: 4x8x64 all-ones -> 64 +- 0.1
+    d, _ = orc.f32_to_f16(1.0 / 127.0)
+    b = np.zeros((8, 34), np.uint8)
+    b[:, 0:2] = np.array([d], np.uint16).view(np.uint8)
+    b[:, 2:] = 127
+    out = ctx.batch_mat_mul(b.reshape(-1), mm.Q8_0, np.ones((8, 64), np.float32), 4, 8, 64)
+    assert np.all(np.abs(out - 64.0) <= 0.1)
+    # qmm.zig:175-211: batch result vs repeated GEMV within 0.01
+    d, _ = orc.f32_to_f16(0.5 / 127.0)
+    b = np.zeros((6, 34), np.uint8)
+    b[:, 0:2] = np.array([d], np.uint16).view(np.uint8)
+    b[:, 2:] = np.array([(i * 32 + j) % 127 for i in range(6) for j in range(32)], np.uint8).reshape(6, 32)
+    raw = b.reshape(-1)
+    bb = ((np.arange(5 * 64) % 7).astype(np.float32) * np.float32(0.3)).reshape(5, 64)
+    out = ctx.batch_mat_mul(raw, mm.Q8_0, bb, 3, 5, 64)
+    for ni in range(5):
+        exp = ctx.mat_vec_mul(raw, mm.Q8_0, bb[ni], 3, 64)
+        assert np.all(np.abs(exp - out[ni]) <= 0.01)
+
+
+def test_seam_is_thread_safe(ctx, orc):
+    """The reference re-enters the seam from 4 pool workers at once
+    (inference.zig:934-971); 4 threads must get the same answers as 1."""
+    rng = np.random.default_rng(10)
+    rows, cols = 256, 1024
+    raws = [_weights(rng, mm.IQ2_XXS, rows, cols) for _ in range(4)]
+    xs = [rng.standard_normal(cols).astype(np.float32) for _ in range(4)]
+    refs = [orc.mat_vec_mul_unified(r, orc.IQ2_XXS, x, rows, cols) for r, x in zip(raws, xs)]
+    errs = []
+
+    def work(i):
+        for _ in range(20):
+            y = ctx.mat_vec_mul(raws[i], mm.IQ2_XXS, xs[i], rows, cols)
+            errs.append(mm.max_abs_rel(y, refs[i]))
+
+    th = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert len(errs) == 80 and max(errs) <= TOL_GEMV
