@@ -188,10 +188,14 @@ int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t 
     g.count = count;
     g.tiles = (rows + 15) / 16;
     g.unit_cols = (type == kIq2Xxs) ? 256 : 64;
-    g.units = (type == kIq2Xxs) ? cols / 256 : ((cols + 31) / 32 + 1) / 2;
+    // Q8_0 tiles hold whole 256-column activation groups (zero units pad).
+    g.units = (type == kIq2Xxs) ? cols / 256 : ((((cols + 31) / 32 + 1) / 2 + 3) / 4) * 4;
     g.cols_pad = g.units * g.unit_cols;
     g.rec_stride = g.tiles * g.units * 64;
-    g.d_stride = g.tiles * g.units * ((type == kIq2Xxs) ? 16 : 32);
+    // Scales are stored per row ([tile][row][unit]) so that one vector load
+    // fetches a row's scales for several units.
+    g.d_row = ((g.units * ((type == kIq2Xxs) ? 1 : 2) + 7) / 8) * 8;
+    g.d_stride = g.tiles * 16 * g.d_row;
     const size_t rec_bytes = (size_t)(g.rec_stride * count * 16);
     const size_t d_bytes = (size_t)(g.d_stride * count * 2);
     e = hipMalloc(&w->recs, rec_bytes);
@@ -201,6 +205,11 @@ int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t 
         return hip_fail(e, "weight: hipMalloc");
     }
     w->bytes = rec_bytes + d_bytes;
+    e = hipMemsetAsync(w->dvals, 0, d_bytes, ctx->stream);  // row padding stays zero
+    if (e != hipSuccess) {
+        weight_destroy(w);
+        return hip_fail(e, "weight: memset");
+    }
     const void* src = raw;
     if (!raw_on_device) {
         e = ctx->d_raw.ensure(raw_bytes);
@@ -250,25 +259,15 @@ int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t 
         return e == hipSuccess ? MMHIP_OK : hip_fail(e, "gemv: launch");
     }
     const TileGeom& g = w->geom;
-    const uint64_t nvec = x_stride ? n : 1;
-    e = qscratch->ensure(quant_act_bytes(nvec, g.cols_pad));
-    if (e != hipSuccess) return hip_fail(e, "gemv: scratch");
-    QuantAct q = quant_act_view(qscratch->p, nvec, g.cols_pad);
-    {
-        TimedLaunch tl(ctx, "quantize");
-        e = launch_quantize(x, x_stride, (uint32_t)nvec, (uint32_t)w->cols, (uint32_t)g.cols_pad, q, ctx->stream);
-    }
-    if (e != hipSuccess) return hip_fail(e, "gemv: quantize");
+    (void)qscratch;
     GemvArgs a;
     a.recs = w->recs;
     a.dvals = w->dvals;
     a.rec_stride = g.rec_stride;
     a.d_stride = g.d_stride;
-    a.xh = q.hi;
-    a.xl = q.lo;
-    a.xs = q.scale;
-    a.xq_stride = x_stride ? q.stride : 0;
-    a.xs_stride = x_stride ? q.scale_stride : 0;
+    a.d_row = (uint32_t)g.d_row;
+    a.x = x;
+    a.x_stride = x_stride;
     a.y = y;
     a.y_stride = y_stride;
     a.tables = ctx->iq2_tables;
@@ -277,6 +276,8 @@ int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t 
     a.tiles = (uint32_t)g.tiles;
     a.units = (uint32_t)g.units;
     a.rows = (uint32_t)g.rows;
+    a.cols = (uint32_t)g.cols;
+    a.tiles_per_wg = 0;
     {
         TimedLaunch tl(ctx, "gemv_q");
         e = launch_gemv_q(a, g.fmt, ctx->num_cu, ctx->stream);

@@ -64,7 +64,7 @@ __global__ void dequant_f16_kernel(const uint16_t* __restrict__ raw, uint64_t n,
 // Raw IQ2_XXS -> tile records (layout in device_common.hpp). One thread per
 // (matrix, row tile, superblock column, lane).
 __global__ void repack_iq2_kernel(const uint8_t* __restrict__ raw, uint64_t rows, uint64_t nsb,
-                                  uint64_t tiles, uint64_t total, uint4* __restrict__ recs,
+                                  uint64_t tiles, uint64_t total, uint64_t d_row, uint4* __restrict__ recs,
                                   uint16_t* __restrict__ dvals) {
     uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= total) return;
@@ -80,26 +80,33 @@ __global__ void repack_iq2_kernel(const uint8_t* __restrict__ raw, uint64_t rows
     if (row < rows) {
         const uint8_t* sb = raw + ((mat * rows + row) * nsb + j) * 66;
         dbits = ld16(sb);
+        uint32_t la = 0, lb = 0;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             uint32_t a0 = ld32u(sb + 2 + 8 * s);
             uint32_t a1 = ld32u(sb + 2 + 8 * s + 4);
             uint32_t idx = (a0 >> (8 * g)) & 0xFFu;
             uint32_t code = (a1 >> (7 * g)) & 0x7Fu;
-            uint32_t ls = a1 >> 28;
+            if ((uint32_t)s == g) la = a1 >> 28;
+            if ((uint32_t)s == 4 + g) lb = a1 >> 28;
             uint32_t rec = (code & 7u) | ((uint32_t)(__popc(code & 15u) & 1) << 3) | (idx << 4) |
-                           (((code >> 4) & 7u) << 12) | (((ls >> g) & 1u) << 15);
-            w[s >> 1] |= rec << (16 * (s & 1));
+                           (((code >> 4) & 7u) << 12);
+            w[s >> 1] |= rec << ((s & 1) ? 17 : 2);
         }
+        // ls of sub-block g in dwords 0,1 and of sub-block 4+g in dwords 2,3.
+        w[0] |= la & 3u;
+        w[1] |= la >> 2;
+        w[2] |= lb & 3u;
+        w[3] |= lb >> 2;
     }
     recs[gid] = make_uint4(w[0], w[1], w[2], w[3]);
-    if (g == 0) dvals[unit * 16 + n] = (uint16_t)dbits;
+    if (g == 0) dvals[((mat * tiles + t) * 16 + n) * d_row + j] = (uint16_t)dbits;
 }
 
 // Raw Q8_0 -> tile records: a unit is two 32-column blocks of 16 rows.
 __global__ void repack_q8_kernel(const uint8_t* __restrict__ raw, uint64_t rows, uint64_t nb,
-                                 uint64_t nu, uint64_t tiles, uint64_t total, uint4* __restrict__ recs,
-                                 uint16_t* __restrict__ dvals) {
+                                 uint64_t nu, uint64_t tiles, uint64_t total, uint64_t d_row,
+                                 uint4* __restrict__ recs, uint16_t* __restrict__ dvals) {
     uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= total) return;
     uint32_t lane = (uint32_t)(gid & 63);
@@ -124,8 +131,9 @@ __global__ void repack_q8_kernel(const uint8_t* __restrict__ raw, uint64_t rows,
     }
     recs[gid] = make_uint4(w[0], w[1], w[2], w[3]);
     if (g == 0) {
-        dvals[(unit * 16 + n) * 2] = (uint16_t)dbits[0];
-        dvals[(unit * 16 + n) * 2 + 1] = (uint16_t)dbits[1];
+        uint16_t* dr = dvals + ((mat * tiles + t) * 16 + n) * d_row + 2 * u;
+        dr[0] = (uint16_t)dbits[0];
+        dr[1] = (uint16_t)dbits[1];
     }
 }
 
@@ -180,10 +188,12 @@ hipError_t launch_repack(const void* raw, const TileGeom& g, uint4* recs, uint16
     const int bs = 256;
     unsigned grid = (unsigned)((total + bs - 1) / bs);
     if (g.fmt == kFmtIq2) {
-        repack_iq2_kernel<<<grid, bs, 0, s>>>((const uint8_t*)raw, g.rows, g.units, g.tiles, total, recs, dvals);
+        repack_iq2_kernel<<<grid, bs, 0, s>>>((const uint8_t*)raw, g.rows, g.units, g.tiles, total, g.d_row, recs,
+                                              dvals);
     } else {
         uint64_t nb = (g.cols + 31) / 32;
-        repack_q8_kernel<<<grid, bs, 0, s>>>((const uint8_t*)raw, g.rows, nb, g.units, g.tiles, total, recs, dvals);
+        repack_q8_kernel<<<grid, bs, 0, s>>>((const uint8_t*)raw, g.rows, nb, g.units, g.tiles, total, g.d_row, recs,
+                                             dvals);
     }
     return hipGetLastError();
 }

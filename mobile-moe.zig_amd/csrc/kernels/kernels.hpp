@@ -21,7 +21,8 @@ struct TileGeom {
     uint64_t unit_cols;    // 256 (IQ2_XXS) or 64 (Q8_0)
     uint64_t cols_pad;     // units * unit_cols
     uint64_t rec_stride;   // uint4 records per matrix = tiles * units * 64
-    uint64_t d_stride;     // u16 scales per matrix = tiles * units * (16 | 32)
+    uint64_t d_row;        // u16 scales per row, padded: roundup(units * (1 | 2), 8)
+    uint64_t d_stride;     // u16 scales per matrix = tiles * 16 * d_row
 };
 
 // Quantised activations: 16-bit block fixed point as two int8 digit planes.
@@ -37,15 +38,15 @@ struct GemvArgs {
     const uint4* recs;
     const uint16_t* dvals;
     uint64_t rec_stride, d_stride;
-    const int8_t* xh;
-    const int8_t* xl;
-    const float* xs;
-    uint64_t xq_stride, xs_stride;  // per problem; 0 = one shared vector
+    uint32_t d_row;
+    const float* x;                 // f32 activations, quantised inside the kernel
+    uint64_t x_stride;              // floats between problems' vectors; 0 = shared
     float* y;
     uint64_t y_stride;
     const uint32_t* tables;         // IQ2_XXS LDS tables (32 KiB)
     uint64_t first_mat;
-    uint32_t n_probs, tiles, units, rows;
+    uint32_t n_probs, tiles, units, rows, cols;
+    uint32_t tiles_per_wg;          // set by launch_gemv_q
 };
 
 // Raw GGUF bytes -> f32, bit-exact (dequant.zig:316-390, 632-659).
@@ -59,7 +60,8 @@ hipError_t launch_repack(const void* raw, const TileGeom& g, uint4* recs, uint16
 hipError_t launch_quantize(const float* x, uint64_t x_stride, uint32_t n_vec, uint32_t cols,
                            uint32_t cols_pad, const QuantAct& q, hipStream_t s);
 
-// Quantised-weight GEMV over n_probs matrices in one launch.
+// Quantised-weight GEMV over n_probs matrices in one launch (activations are
+// quantised inside the kernel).
 hipError_t launch_gemv_q(const GemvArgs& a, uint32_t fmt, int num_cu, hipStream_t s);
 
 // Plain f32 / f16 weight GEMV (router, matVecMulUnified's f32 branch):

@@ -1,0 +1,178 @@
+// Per-wave tile products shared by the GEMV, QMM and MoE kernels.
+//
+// Decode (one activation vector, A operand from the LDS A layout):
+//   units_dot_* processes up to 8 record units of one 16-row tile. Each
+//   32-column block is one v_mfma_i32_16x16x32_i8 with A rows 0/1 = the
+//   vector's hi/lo digits; the integer results of four consecutive blocks are
+//   gathered one per 16-lane row (gather_rows4), so every lane group scales and
+//   accumulates a different block: lane (g, n) accumulates blocks with
+//   index % 4 == g of row n. reduce_groups() folds the four partial sums into
+//   lanes 0..15 at the end of a tile.
+//
+// Batched (tiles of 8 activation vectors, A operand from global memory):
+//   tile_mm: lane (g, n) ends with row n . vectors 2g and 2g+1 of every tile.
+#pragma once
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace mmhip {
+
+constexpr int kMaxUnitsPerStep = 8;
+
+__device__ __forceinline__ float reduce_groups(float acc) {
+    acc += __shfl_xor(acc, 16, kWave);
+    acc += __shfl_xor(acc, 32, kWave);
+    return acc;
+}
+
+// All 8 B operands of an IQ2_XXS record unit (LDS table reads).
+__device__ __forceinline__ void iq2_decode_unit(const uint4& rr, const uint32_t* tab, long (&b)[8]) {
+    const uint32_t w4[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) b[s] = (s & 1) ? iq2_bop_hi(w4[s >> 1], tab) : iq2_bop_lo(w4[s >> 1], tab);
+}
+
+// One decode step of UPS record units (compile-time, fully unrolled).
+// IQ2_XXS: unit i is 256-column group ub + i of the LDS activation chunk.
+// Only lanes n = 0, 1 (A rows 0 / 1) carry activation digits; the other
+// lanes' A rows only reach D rows that are never read, so they skip the LDS
+// reads (exec-masked) and keep whatever their registers hold. The B operands
+// of unit i+1 are read from LDS before the MFMAs of unit i issue, so table
+// latency overlaps MFMA and VALU work. xs_g = xs + g.
+template <int UPS>
+__device__ __forceinline__ void step_dot_iq2(const uint4 (&r)[kMaxUnitsPerStep],
+                                             const uint32_t (&dw)[kMaxUnitsPerStep], uint32_t ub,
+                                             const int8_t* a_run, bool has_a, const float* xs_g,
+                                             const uint32_t* tab, float& acc) {
+    long b[2][8];
+    long av[8];
+    iq2_decode_unit(r[0], tab, b[0]);
+#pragma unroll
+    for (int i = 0; i < UPS; ++i) {
+        const int cur = i & 1, nxt = cur ^ 1;
+        if (has_a) lds_a_group(av, a_run, ub + i);
+        if (i + 1 < UPS) iq2_decode_unit(r[i + 1], tab, b[nxt]);
+        const uint32_t blk0 = (ub + i) * 8;
+        int v[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const v4i dv = mfma_i8(av[s], b[cur][s]);
+            v[s] = digits_combine(dv[0], dv[1]);
+        }
+        const int w0 = gather_rows4(v[0], v[1], v[2], v[3]);
+        const int w1 = gather_rows4(v[4], v[5], v[6], v[7]);
+        const float dq = f16_scale(dw[i]) * 0.25f;
+        const float hdq = dq * 0.5f;
+        const float c0 = fmaf((float)iq2_ls_a(r[i]), dq, hdq) * xs_g[blk0];
+        const float c1 = fmaf((float)iq2_ls_b(r[i]), dq, hdq) * xs_g[blk0 + 4];
+        acc = fmaf((float)w0, c0, acc);
+        acc = fmaf((float)w1, c1, acc);
+    }
+}
+
+// Q8_0: units in pairs (four 32-column blocks per gather); a pair is half of
+// a 256-column A group. UPS is 4 or 8 and ub a multiple of 4, so steps start
+// on A-group boundaries.
+template <int UPS>
+__device__ __forceinline__ void step_dot_q8(const uint4 (&r)[kMaxUnitsPerStep],
+                                            const uint32_t (&dw)[kMaxUnitsPerStep], uint32_t ub,
+                                            const int8_t* a_run, bool has_a, const float* xs_g, uint32_t g,
+                                            float& acc) {
+    long av[8];
+#pragma unroll
+    for (int i = 0; i < UPS; i += 2) {
+        const bool two = i + 1 < UPS;
+        const uint32_t blk0 = (ub + i) * 2;
+        if ((i & 3) == 0 && has_a) lds_a_group(av, a_run, blk0 >> 3);
+        const int half = (i >> 1) & 1;
+        int v[4];
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            if (bb >= 2 && !two) {
+                v[bb] = 0;
+                continue;
+            }
+            const uint4& rr = r[i + (bb >> 1)];
+            const long bop = (bb & 1) ? (long)(((uint64_t)rr.w << 32) | rr.z) : (long)(((uint64_t)rr.y << 32) | rr.x);
+            const v4i dv = mfma_i8(av[4 * half + bb], bop);
+            v[bb] = digits_combine(dv[0], dv[1]);
+        }
+        const int w = gather_rows4(v[0], v[1], v[2], v[3]);
+        // lane group g scales block blk0 + g: unit i + g/2, half g&1
+        const uint32_t dsel = (g >= 2) ? (two ? dw[i + 1 < UPS ? i + 1 : i] : 0u) : dw[i];
+        const float d = f16_scale((dsel >> (16 * (g & 1))) & 0xFFFFu);
+        const float c = (g >= 2 && !two) ? 0.0f : d * xs_g[blk0];
+        acc = fmaf((float)w, c, acc);
+    }
+}
+
+// Activation source of one lane for TT vector tiles (batched products):
+// a_row[tt] is the lane's A digit row (vector tt*8 + n/2, plane n&1, offset
+// 8g) or nullptr when that vector does not exist; s0/s1[tt] are the block-
+// scale rows of vectors tt*8 + 2g and tt*8 + 2g + 1 (any valid row when
+// absent: their A rows are zero).
+template <int TT>
+struct ActTiles {
+    const int8_t* a_row[TT];
+    const float* s0[TT];
+    const float* s1[TT];
+};
+
+// Scale word of unit u in a row's scale run (layout [tile][row][unit]):
+// IQ2_XXS one f16, Q8_0 two f16 (blocks 2u, 2u+1) in one u32.
+template <int FMT>
+__device__ __forceinline__ uint32_t unit_dbits(const uint16_t* Drow, uint32_t u) {
+    if (FMT == kFmtIq2) return (uint32_t)Drow[u];
+    return reinterpret_cast<const uint32_t*>(Drow)[u];
+}
+
+// R: this lane's record pointer for unit 0 of the tile; Drow: this lane's
+// row scale run.
+template <int FMT, int TT>
+__device__ __forceinline__ void tile_mm(const uint4* __restrict__ R, const uint16_t* __restrict__ Drow,
+                                        uint32_t units, const ActTiles<TT>& act, const uint32_t* tab,
+                                        uint32_t lane, float (&acc)[TT][2]) {
+    const uint32_t g = lane >> 4;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[tt][0] = acc[tt][1] = 0.0f;
+    for (uint32_t u = 0; u < units; ++u) {
+        const uint4 r = R[(uint64_t)u * 64];
+        const uint32_t dw = unit_dbits<FMT>(Drow, u);
+        if (FMT == kFmtIq2) {
+            const uint32_t ls = iq2_ls_all(r, g);
+            const float dq = f16_scale(dw) * 0.25f;
+            const float hdq = dq * 0.5f;
+            const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll 2
+            for (int s = 0; s < 8; ++s) {
+                const long bop = (s & 1) ? iq2_bop_hi(w4[s >> 1], tab) : iq2_bop_lo(w4[s >> 1], tab);
+                const uint32_t blk = u * 8 + s;
+                const float cw = fmaf((float)((ls >> (4 * s)) & 15u), dq, hdq);
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt) {
+                    const long aop = act.a_row[tt] ? *reinterpret_cast<const long*>(act.a_row[tt] + blk * 32) : 0;
+                    const v4i dv = mfma_i8(aop, bop);
+                    acc[tt][0] = fmaf((float)digits_combine(dv[0], dv[1]), cw * act.s0[tt][blk], acc[tt][0]);
+                    acc[tt][1] = fmaf((float)digits_combine(dv[2], dv[3]), cw * act.s1[tt][blk], acc[tt][1]);
+                }
+            }
+        } else {
+            const long bops[2] = {(long)(((uint64_t)r.y << 32) | r.x), (long)(((uint64_t)r.w << 32) | r.z)};
+            const float cws[2] = {f16_scale(dw & 0xFFFFu), f16_scale(dw >> 16)};
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const uint32_t blk = 2 * u + b;
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt) {
+                    const long aop = act.a_row[tt] ? *reinterpret_cast<const long*>(act.a_row[tt] + blk * 32) : 0;
+                    const v4i dv = mfma_i8(aop, bops[b]);
+                    acc[tt][0] = fmaf((float)digits_combine(dv[0], dv[1]), cws[b] * act.s0[tt][blk], acc[tt][0]);
+                    acc[tt][1] = fmaf((float)digits_combine(dv[2], dv[3]), cws[b] * act.s1[tt][blk], acc[tt][1]);
+                }
+            }
+        }
+    }
+}
+
+}  // namespace mmhip
