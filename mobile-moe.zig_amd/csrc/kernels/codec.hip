@@ -9,10 +9,6 @@ namespace {
 
 constexpr uint32_t kTypeF32 = 0, kTypeF16 = 1, kTypeQ8_0 = 8, kTypeIq2 = 16;
 
-__constant__ uint64_t c_grid[256] = {
-#include "../iq2xxs_grid.inc"
-};
-
 // Raw GGUF bytes are only 2-byte aligned (34 / 66-byte blocks): read u16s.
 __device__ __forceinline__ uint32_t ld16(const uint8_t* p) {
     return (uint32_t)*reinterpret_cast<const uint16_t*>(p);
@@ -43,7 +39,7 @@ __global__ void dequant_iq2_kernel(const uint8_t* __restrict__ raw, uint64_t n, 
     uint32_t a0 = ld32u(blk + 2 + 8 * ib);
     uint32_t a1 = ld32u(blk + 2 + 8 * ib + 4);
     float db = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
-    uint64_t gv = c_grid[(a0 >> (8 * l)) & 0xFFu];
+    uint64_t gv = c_iq2_grid[(a0 >> (8 * l)) & 0xFFu];
     uint32_t code = (a1 >> (7 * l)) & 0x7Fu;
     uint32_t s = code | ((uint32_t)(__popc(code) & 1) << 7);
 #pragma unroll

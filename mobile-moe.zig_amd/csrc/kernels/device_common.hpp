@@ -77,6 +77,52 @@ __device__ __forceinline__ float f16_scale(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short)h));
 }
 
+// Workgroup barrier that orders LDS only. __syncthreads() is a workgroup-
+// scope fence on all memory, which makes every wave wait for all of its
+// outstanding global loads (the prefetched weight stream) at the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Raw buffer loads. A load whose offset lies beyond the resource's size
+// returns zeros without a memory access, so kernels issue every load
+// unconditionally (steps past a wave's end, columns past the vector's end)
+// and the compiler's load counters stay exact: vector-load waits complete in
+// issue order, and a load under a branch makes every later wait count as if
+// it had not been issued. Resources here are below 2 GiB, so kBufOob is out
+// of range for all of them.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+constexpr uint32_t kBufWord3 = 0x00020000u;  // word 3 of a raw buffer resource (32-bit data format)
+constexpr uint32_t kBufOob = 0x80000000u;
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kBufWord3);
+}
+// Cache policy of a load: kCacheNormal, or kCacheStream (non-temporal) for
+// data read exactly once (weights), so that it does not evict the small
+// shared data (activations, grid) that every workgroup reads.
+constexpr int kCacheNormal = 0;
+constexpr int kCacheStream = 2;
+template <int POL = kCacheNormal>
+__device__ __forceinline__ uint4 buf_load_b128(BufRsrc r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+template <int POL = kCacheNormal>
+__device__ __forceinline__ uint2 buf_load_b64(BufRsrc r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, POL);
+    return make_uint2(v[0], v[1]);
+}
+template <int POL = kCacheNormal>
+__device__ __forceinline__ uint32_t buf_load_b32(BufRsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL);
+}
+template <int POL = kCacheNormal>
+__device__ __forceinline__ uint32_t buf_load_b16(BufRsrc r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, POL);
+}
+
 __device__ __forceinline__ v4i mfma_i8(long a, long b) {
     v4i z = {0, 0, 0, 0};
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
@@ -122,11 +168,59 @@ __device__ __forceinline__ int gather_rows4(int v0, int v1, int v2, int v3) {
     return (int)r[0];
 }
 
-// Cooperative copy of the 32 KiB IQ2_XXS sign/grid tables into LDS.
-__device__ __forceinline__ void load_iq2_tables(uint32_t* lds, const uint32_t* __restrict__ g) {
-    const uint4* src = reinterpret_cast<const uint4*>(g);
-    uint4* dst = reinterpret_cast<uint4*>(lds);
-    for (int i = threadIdx.x; i < kIq2TableWords / 4; i += blockDim.x) dst[i] = src[i];
+// The IQ2_XXS grid (dequant.zig:148-213): 256 entries of 8 magnitudes.
+static __constant__ uint64_t c_iq2_grid[256] = {
+#include "../iq2xxs_grid.inc"
+};
+
+// 0xFF in every byte whose bit is set in the 4-bit sign nibble m.
+__host__ __device__ constexpr uint32_t nibble_byte_mask(uint32_t m) {
+    return ((m & 1u) ? 0xFFu : 0u) | ((m & 2u) ? 0xFF00u : 0u) | ((m & 4u) ? 0xFF0000u : 0u) |
+           ((m & 8u) ? 0xFF000000u : 0u);
+}
+__host__ __device__ constexpr uint32_t parity3(uint32_t v) { return (v ^ (v >> 1) ^ (v >> 2)) & 1u; }
+// Negates the bytes selected by mask (0xFF per byte). Grid magnitudes are at
+// most 0x2B, so (b ^ 0xFF) + 1 never carries into the next byte.
+__device__ __forceinline__ uint32_t negate_bytes(uint32_t w, uint32_t mask) {
+    return (w ^ mask) + (mask & 0x01010101u);
+}
+
+// Builds the 32 KiB sign/grid tables (layout above) in LDS from the 2 KiB
+// grid, for blocks of 256, 512 or 768 threads: thread t handles grid index
+// t % 256; with 256 threads it writes LO[idx * 16 .. +15] and the 16 HI words
+// of idx, with more threads threads 0..255 write LO, 256..511 HI.
+// iq2_grid_entry issues the thread's grid load (put it ahead of the kernel's
+// bulk loads: waits on vector loads complete in issue order);
+// build_iq2_tables writes the tables. The caller synchronises before the
+// first lookup.
+__device__ __forceinline__ uint64_t iq2_grid_entry() { return c_iq2_grid[threadIdx.x & 255u]; }
+
+template <int WG>
+__device__ __forceinline__ void build_iq2_tables(uint32_t* tab, uint64_t gv) {
+    static_assert(WG == 256 || WG == 512 || WG == 768, "table build assumes 256, 512 or 768 threads");
+    const uint32_t idx = threadIdx.x & 255u;
+    if (WG == 256 || threadIdx.x < 256) {
+        const uint32_t lo = (uint32_t)gv;
+        uint32_t w[16];
+#pragma unroll
+        for (uint32_t e = 0; e < 16; ++e) {
+            const uint32_t b012 = e & 7u, par = e >> 3;
+            w[e] = negate_bytes(lo, nibble_byte_mask(b012 | ((par ^ parity3(b012)) << 3)));
+        }
+        uint4* d = reinterpret_cast<uint4*>(tab + idx * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) d[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+    }
+    if (WG == 256 || (threadIdx.x >= 256 && threadIdx.x < 512)) {
+        const uint32_t hi = (uint32_t)(gv >> 32);
+#pragma unroll
+        for (uint32_t h3 = 0; h3 < 8; ++h3) {
+            uint2 v;
+            v.x = negate_bytes(hi, nibble_byte_mask(h3 | (parity3(h3) << 3)));
+            v.y = negate_bytes(hi, nibble_byte_mask(h3 | ((1u ^ parity3(h3)) << 3)));
+            *reinterpret_cast<uint2*>(tab + 4096 + h3 * 512 + idx * 2) = v;
+        }
+    }
 }
 
 // Wave-wide sum (all 64 lanes receive the result).
@@ -153,8 +247,8 @@ __device__ __forceinline__ float quantize_block32(float x, int8_t* hi, int8_t* l
         scale = 0.0f;
         inv = 0.0f;
     } else {
-        scale = a / kDigitMax;
-        inv = kDigitMax / a;
+        scale = a * (1.0f / kDigitMax);
+        inv = __builtin_amdgcn_rcpf(scale);
     }
     float qf = rintf(x * inv);
     qf = fminf(fmaxf(qf, -kDigitMax), kDigitMax);
@@ -165,33 +259,83 @@ __device__ __forceinline__ float quantize_block32(float x, int8_t* hi, int8_t* l
     return scale;
 }
 
-// Quantise x[0..cols) into the LDS A layout (kAGroupBytes per 256 columns)
-// plus block scales xs[nblk]; blocks cover [0, nblk * 32), zero-padded. All
-// threads of the block take part; the caller synchronises afterwards.
-__device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, uint32_t cols, uint32_t nblk,
-                                                int8_t* aq, float* xs) {
-    constexpr int kBatch = 8;  // blocks per 32-lane group whose loads are in flight together
-    const uint32_t groups = blockDim.x >> 5;
-    const uint32_t j = threadIdx.x & 31;
-    const uint32_t g = j >> 3, jj = j & 7;
-    for (uint32_t b0 = threadIdx.x >> 5; b0 < nblk; b0 += groups * kBatch) {
-        float v[kBatch];
+// Max over each aligned group of 8 lanes (DPP: quad swaps, then the
+// half-row mirror); every lane of the group receives it. All 64 lanes must be
+// active.
+__device__ __forceinline__ float max8_lanes(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    return v;
+}
+
+// Activation quantisation for the decode kernels: one 32-column block per 8
+// lanes, 4 columns per lane. A block's scale is s = max|x| / 32512 and each
+// column becomes q = rint(x / s) in [-32512, 32512], split into int8 digits
+// hi = (q + 128) >> 8 and lo = q - 256 hi (x ~= s (256 hi + lo)). Blocks whose
+// max |x| is non-finite (NaN counts as Inf) get a NaN scale, which poisons
+// every output that reads them; blocks below 2^-100 are all zero. The
+// reciprocal need not be correctly rounded: q is clamped, and the error stays
+// far below the half-step rounding error.
+__device__ __forceinline__ float quantize_quad(const float (&v)[4], uint32_t& hi4, uint32_t& lo4) {
+    float m = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-            const uint32_t c = (b0 + i * groups) * 32 + j;
-            v[i] = (b0 + i * groups < nblk && c < cols) ? x[c] : 0.0f;
-        }
+    for (int e = 0; e < 4; ++e) m = fmaxf(m, (v[e] != v[e]) ? __uint_as_float(0x7F800000u) : fabsf(v[e]));
+    m = max8_lanes(m);
+    float scale, inv;
+    if (!(m <= 3.4028235e38f)) {
+        scale = __uint_as_float(0x7FC00000u);
+        inv = 0.0f;
+    } else if (m < 0x1p-100f) {
+        scale = 0.0f;
+        inv = 0.0f;
+    } else {
+        scale = m * (1.0f / kDigitMax);
+        inv = __builtin_amdgcn_rcpf(scale);
+    }
+    hi4 = 0;
+    lo4 = 0;
 #pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-            const uint32_t b = b0 + i * groups;
-            if (b >= nblk) break;
-            int8_t h, l;
-            const float s = quantize_block32(v[i], &h, &l);
-            int8_t* run = aq + (b >> 3) * kAGroupBytes + g * kARun + (b & 7) * 8 + jj;
-            run[0] = h;
-            run[4 * kARun] = l;
-            if (j == 0) xs[b] = s;
-        }
+    for (int e = 0; e < 4; ++e) {
+        const float qf = fminf(fmaxf(rintf(v[e] * inv), -kDigitMax), kDigitMax);
+        const int q = (inv == 0.0f) ? 0 : (int)qf;
+        const int h = (q + 128) >> 8;
+        const int l = q - h * 256;
+        hi4 |= (uint32_t)(h & 0xFF) << (8 * e);
+        lo4 |= (uint32_t)(l & 0xFF) << (8 * e);
+    }
+    return scale;
+}
+
+// A pass covers WG / 8 blocks: thread t quantises columns 4 (t & 7) .. +3 of
+// block b0 + t / 8. x_pass_load issues the loads (xr covers the vector's
+// cols floats; columns beyond read as zero), x_pass_store quantises into the
+// LDS A layout (kAGroupBytes per 256 columns) and the block scales xs[];
+// blocks at or beyond nblk are not stored. Every thread of the block must
+// call both (the max uses DPP).
+__device__ __forceinline__ void x_pass_load(BufRsrc xr, uint32_t b0, float (&v)[4]) {
+    const uint32_t off = ((b0 + (threadIdx.x >> 3)) * 32 + 4 * (threadIdx.x & 7)) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(buf_load_b32(xr, off + 4 * e, 0));
+}
+__device__ __forceinline__ void x_pass_store(const float (&v)[4], uint32_t nblk, uint32_t b0, int8_t* aq, float* xs) {
+    uint32_t h4, l4;
+    const float s = quantize_quad(v, h4, l4);
+    const uint32_t b = b0 + (threadIdx.x >> 3), jq = threadIdx.x & 7;
+    if (b < nblk) {
+        int8_t* run = aq + (b >> 3) * kAGroupBytes + (jq >> 1) * kARun + (b & 7) * 8 + 4 * (jq & 1);
+        *reinterpret_cast<uint32_t*>(run) = h4;
+        *reinterpret_cast<uint32_t*>(run + 4 * kARun) = l4;
+        if (jq == 0) xs[b] = s;
+    }
+}
+// Whole activation chunk: blocks [0, nblk) of the vector behind xr.
+template <int WG>
+__device__ __forceinline__ void quantize_to_lds(BufRsrc xr, uint32_t nblk, int8_t* aq, float* xs) {
+    for (uint32_t b0 = 0; b0 < nblk; b0 += WG / 8) {
+        float v[4];
+        x_pass_load(xr, b0, v);
+        x_pass_store(v, nblk, b0, aq, xs);
     }
 }
 

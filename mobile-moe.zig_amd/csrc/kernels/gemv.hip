@@ -3,10 +3,10 @@
 // Quantised weights (Q8_0, IQ2_XXS): a workgroup owns one activation vector
 // (problem) and a contiguous range of 16-row tiles. It quantises the vector
 // into LDS (the A operand of every MFMA, so the separate quantisation launch
-// disappears), copies the 32 KiB IQ2_XXS sign/grid tables into LDS, and each
-// wave then streams its tiles' 1 KiB record units with one 128-bit load per
-// lane, double-buffered so the next step's loads are in flight while the
-// current one computes. Every weight byte is read exactly once.
+// disappears), builds the 32 KiB IQ2_XXS sign/grid tables in LDS from the
+// 2 KiB grid, and each wave then streams its tiles' 1 KiB record units with one 128-bit load per
+// lane, through a ring of three register buffers so the next two steps'
+// loads are in flight while the current one computes. Every weight byte is read exactly once.
 //
 // f32 / f16 weights (the router, matVecMulUnified's f32 branch): one wave
 // per output row.
@@ -15,6 +15,8 @@
 #include "tile_ops.hpp"
 
 #include <cstdlib>
+#include <map>
+#include <mutex>
 
 namespace mmhip {
 
@@ -22,42 +24,62 @@ namespace {
 
 constexpr uint32_t kChunkBlocks = 256;  // 8192 columns of activation per LDS chunk (multiple of 8)
 
-// One step's records (UPS units) and the row's scale words for them.
+// One step's records (UPS units, 1 KiB apart) and the row's scale words for
+// them. rec_soff / d_soff are the step's uniform byte offsets (kBufOob for a
+// step past the wave's end); rec_voff = lane * 16, d_voff = the row's scale
+// run. Scale runs are 16-byte aligned rows of d_row u16.
 template <int FMT, int UPS>
-__device__ __forceinline__ void load_step(const uint4* R, const uint16_t* Drow, uint32_t u_first,
-                                          uint4 (&r)[kMaxUnitsPerStep], uint32_t (&dw)[kMaxUnitsPerStep]) {
+__device__ __forceinline__ void load_step(BufRsrc rr, uint32_t rec_voff, uint32_t rec_soff, BufRsrc dr,
+                                          uint32_t d_voff, uint32_t d_soff, uint4 (&r)[kMaxUnitsPerStep],
+                                          uint32_t (&dw)[kMaxUnitsPerStep]) {
 #pragma unroll
-    for (int i = 0; i < UPS; ++i) r[i] = R[(uint64_t)(u_first + i) * 64];
-    // Scale runs are 16-byte aligned rows; vector loads where the step size allows.
-    if (FMT == kFmtIq2 && (UPS == 8 || UPS == 6)) {
-        const uint4 q = *reinterpret_cast<const uint4*>(Drow + u_first);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    for (int i = 0; i < UPS; ++i) r[i] = buf_load_b128<kCacheStream>(rr, rec_voff + i * 1024, rec_soff);
+    if (FMT == kFmtIq2) {
+        // Kept packed (two f16 per dword, see iq2_scale_bits): unpacking at
+        // the load would make the compiler wait for the data right there.
+        if (UPS == 8) {
+            const uint4 q = buf_load_b128<kCacheStream>(dr, d_voff, d_soff);
+            dw[0] = q.x;
+            dw[1] = q.y;
+            dw[2] = q.z;
+            dw[3] = q.w;
+        } else if (UPS == 4) {
+            const uint2 q = buf_load_b64<kCacheStream>(dr, d_voff, d_soff);
+            dw[0] = q.x;
+            dw[1] = q.y;
+        } else if (UPS == 2) {
+            dw[0] = buf_load_b32<kCacheStream>(dr, d_voff, d_soff);
+        } else {
 #pragma unroll
-        for (int i = 0; i < UPS; ++i) dw[i] = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-    } else if (FMT == kFmtIq2 && UPS == 4) {
-        const uint2 q = *reinterpret_cast<const uint2*>(Drow + u_first);
-        const uint32_t w[2] = {q.x, q.y};
-#pragma unroll
-        for (int i = 0; i < UPS; ++i) dw[i] = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-    } else if (FMT == kFmtQ8 && (UPS == 4 || UPS == 8)) {
+            for (int i = 0; i < UPS; ++i) dw[i] = buf_load_b16<kCacheStream>(dr, d_voff + 2 * i, d_soff);
+        }
+    } else {
+        // Q8_0: one u32 (two f16) per unit; steps of 4 or 8 units start on
+        // 16-byte boundaries.
 #pragma unroll
         for (int h = 0; h < UPS / 4; ++h) {
-            const uint4 q = *reinterpret_cast<const uint4*>(Drow + 2 * (u_first + 4 * h));
+            const uint4 q = buf_load_b128<kCacheStream>(dr, d_voff + 16 * h, d_soff);
             dw[4 * h] = q.x;
             dw[4 * h + 1] = q.y;
             dw[4 * h + 2] = q.z;
             dw[4 * h + 3] = q.w;
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < UPS; ++i) dw[i] = unit_dbits<FMT>(Drow, u_first + i);
     }
 }
 
 // UPS = record units per step (compile-time); a tile's units in a K-chunk
 // are a whole number of steps. WG threads per workgroup.
+//
+// Loads: every weight, scale and activation load goes through a buffer
+// resource and is issued unconditionally (out-of-range offsets for steps past
+// the wave's end), so each wait covers exactly the loads it needs. The
+// prologue issues the grid entry and the activation loads of all waves first,
+// then the first three steps' weights, and only then waits on the small
+// loads.
+// A ring of three register buffers keeps the next two steps' loads in flight
+// while a step computes.
 template <int FMT, int UPS, int WG>
-__global__ __launch_bounds__(WG, (WG == 256 ? 4 : 2)) void gemv_q_kernel(GemvArgs a) {
+__global__ __launch_bounds__(WG, (WG == 256 ? 3 : WG == 512 ? 2 : 1)) void gemv_q_kernel(GemvArgs a) {
     constexpr uint32_t kWaves = WG / 64;
     // Static LDS for the tables (known address: table offsets fold into the
     // ds_read immediates); dynamic LDS for the activation chunk.
@@ -72,7 +94,7 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 4 : 2)) void gemv_q_kernel(GemvArg
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t n = lane & 15, g = lane >> 4;
-    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t p = blockIdx.y;
     const uint64_t mat = a.first_mat + p;
     const float* x = a.x + (uint64_t)p * a.x_stride;
@@ -86,8 +108,10 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 4 : 2)) void gemv_q_kernel(GemvArg
     const bool has_a = n < 2;
     const int8_t* a_run = aq + (n & 1) * 4 * kARun + g * kARun;  // used by lanes n < 2 only
     const float* xs_g = xs + g;
-    const uint4* rec0 = a.recs + mat * a.rec_stride + lane;
-    const uint16_t* drow0 = a.dvals + mat * a.d_stride + (uint64_t)n * a.d_row;
+    const BufRsrc rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
+    const BufRsrc d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
+    const uint32_t rec_voff = lane * 16;
+    const uint32_t d_voff = n * a.d_row * 2;
 
     // Step s of a K-chunk starting at unit u_begin: tile i = s / n_sub,
     // units [u_begin + UPS * (s % n_sub), +UPS).
@@ -95,50 +119,86 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 4 : 2)) void gemv_q_kernel(GemvArg
     uint32_t n_sub = min(a.units, chunk_units) / UPS;
     auto tile_of = [&](uint32_t s) { return t_begin + wave + kWaves * (s / n_sub); };
     auto first_unit = [&](uint32_t s) { return u_begin + (s % n_sub) * UPS; };
-    uint4 r[kMaxUnitsPerStep];
-    uint32_t dw[kMaxUnitsPerStep];
-    auto load = [&](uint32_t s) {
-        const uint32_t t = tile_of(s);
-        load_step<FMT, UPS>(rec0 + (uint64_t)t * a.units * 64, drow0 + (uint64_t)t * 16 * a.d_row, first_unit(s), r,
-                            dw);
-    };
-
-    // The first step's weight loads go out before the prologue, so HBM
-    // latency overlaps the table copy and the activation quantisation.
     uint32_t steps = my_n * n_sub;
-    if (steps > 0) load(0);
-    if (FMT == kFmtIq2) load_iq2_tables(tab, a.tables);
-
-    for (uint32_t kb = 0; kb < nblk_all; kb += chunk_blk) {
-        const uint32_t nb = min(chunk_blk, nblk_all - kb);
-        if (kb > 0) {
-            __syncthreads();  // previous chunk's LDS no longer in use
-            u_begin = kb / kBlkPerUnit;
-            n_sub = (nb / kBlkPerUnit) / UPS;
-            steps = my_n * n_sub;
-            if (steps > 0) load(0);
+    uint4 r0[kMaxUnitsPerStep], r1[kMaxUnitsPerStep], r2[kMaxUnitsPerStep];
+    uint32_t d0[kMaxUnitsPerStep], d1[kMaxUnitsPerStep], d2[kMaxUnitsPerStep];
+    auto load = [&](uint32_t s, uint4 (&r)[kMaxUnitsPerStep], uint32_t (&dw)[kMaxUnitsPerStep]) {
+        uint32_t rs = kBufOob, ds = kBufOob;
+        if (s < steps) {
+            const uint32_t t = tile_of(s), u = first_unit(s);
+            rs = (t * a.units + u) * 1024;
+            ds = (t * 16 * a.d_row + u * (FMT == kFmtIq2 ? 1 : 2)) * 2;
         }
-        quantize_to_lds(x + kb * 32, a.cols > kb * 32 ? a.cols - kb * 32 : 0, nb, aq, xs);
-        __syncthreads();
-
-        float acc = 0.0f;
-        for (uint32_t s = 0; s < steps; ++s) {
-            if (s > 0) load(s);
-            const uint32_t ub = first_unit(s) - u_begin;  // unit index within the LDS chunk
-            if (FMT == kFmtIq2)
-                step_dot_iq2<UPS>(r, dw, ub, a_run, has_a, xs_g, tab, acc);
-            else
-                step_dot_q8<UPS>(r, dw, ub, a_run, has_a, xs_g, g, acc);
-            if (s % n_sub == n_sub - 1) {
-                const float tot = reduce_groups(acc);
-                acc = 0.0f;
-                const uint32_t row = tile_of(s) * 16 + n;
-                if (lane < 16 && row < a.rows) {
-                    float* yp = a.y + (uint64_t)p * a.y_stride + row;
-                    *yp = (kb == 0) ? tot : *yp + tot;
-                }
+        load_step<FMT, UPS>(rec_r, rec_voff, rs, d_r, d_voff, ds, r, dw);
+    };
+    float acc = 0.0f;
+    uint32_t kb = 0;
+    // Computes step s from (r, dw); writes the tile's row sums after its last step.
+    auto compute = [&](uint32_t s, const uint4 (&r)[kMaxUnitsPerStep], const uint32_t (&dw)[kMaxUnitsPerStep]) {
+        const uint32_t ub = first_unit(s) - u_begin;  // unit index within the LDS chunk
+        if (FMT == kFmtIq2)
+            step_dot_iq2<UPS>(r, dw, ub, a_run, has_a, xs_g, tab, acc);
+        else
+            step_dot_q8<UPS>(r, dw, ub, a_run, has_a, xs_g, g, acc);
+        if (s % n_sub == n_sub - 1) {
+            const float tot = reduce_groups(acc);
+            acc = 0.0f;
+            const uint32_t row = tile_of(s) * 16 + n;
+            if (lane < 16 && row < a.rows) {
+                float* yp = a.y + (uint64_t)p * a.y_stride + row;
+                *yp = (kb == 0) ? tot : *yp + tot;
             }
         }
+    };
+
+    {
+        // Prologue of the first chunk (two activation passes cover 32 * WG / 4
+        // columns; longer chunks quantise the rest after the weight loads).
+        const uint32_t nb = chunk_blk;
+        const BufRsrc x_r = make_rsrc(x, min(a.cols, chunk_blk * 32) * 4);
+        uint64_t gv = 0;
+        if (FMT == kFmtIq2) gv = iq2_grid_entry();
+        float xv0[4], xv1[4];
+        x_pass_load(x_r, 0, xv0);
+        x_pass_load(x_r, WG / 8, xv1);
+        // A CU serves its waves' loads in issue order: the barrier (no memory
+        // fence, no wait) puts every wave's small loads ahead of the weights.
+        __builtin_amdgcn_s_barrier();
+        load(0, r0, d0);
+        load(1, r1, d1);
+        load(2, r2, d2);
+        if (FMT == kFmtIq2) build_iq2_tables<WG>(tab, gv);
+        x_pass_store(xv0, nb, 0, aq, xs);
+        x_pass_store(xv1, nb, WG / 8, aq, xs);
+        for (uint32_t b0 = 2 * (WG / 8); b0 < nb; b0 += WG / 8) {
+            float v[4];
+            x_pass_load(x_r, b0, v);
+            x_pass_store(v, nb, b0, aq, xs);
+        }
+    }
+    for (;;) {
+        lds_barrier();
+        for (uint32_t s = 0; s < steps; s += 3) {
+            compute(s, r0, d0);
+            load(s + 3, r0, d0);
+            if (s + 1 < steps) compute(s + 1, r1, d1);
+            load(s + 4, r1, d1);
+            if (s + 2 < steps) compute(s + 2, r2, d2);
+            load(s + 5, r2, d2);
+        }
+        kb += chunk_blk;
+        if (kb >= nblk_all) break;
+        // Next K-chunk (activations longer than one LDS chunk).
+        const uint32_t nb = min(chunk_blk, nblk_all - kb);
+        lds_barrier();  // previous chunk's LDS no longer in use
+        u_begin = kb / kBlkPerUnit;
+        n_sub = (nb / kBlkPerUnit) / UPS;
+        steps = my_n * n_sub;
+        load(0, r0, d0);
+        load(1, r1, d1);
+        load(2, r2, d2);
+        const uint32_t c0 = kb * 32;
+        quantize_to_lds<WG>(make_rsrc(x + c0, (a.cols > c0 ? min(a.cols - c0, nb * 32) : 0) * 4), nb, aq, xs);
     }
 }
 
@@ -196,16 +256,16 @@ static int pick_ups(uint32_t fmt, uint32_t units) {
 }
 
 template <int FMT, int WG>
-static void launch_ups(int ups, dim3 grid, size_t lds, hipStream_t s, const GemvArgs& a) {
+static const void* kernel_for(int ups) {
     switch (ups) {
-        case 1: gemv_q_kernel<FMT, 1, WG><<<grid, WG, lds, s>>>(a); break;
-        case 2: gemv_q_kernel<FMT, 2, WG><<<grid, WG, lds, s>>>(a); break;
-        case 3: gemv_q_kernel<FMT, 3, WG><<<grid, WG, lds, s>>>(a); break;
-        case 4: gemv_q_kernel<FMT, 4, WG><<<grid, WG, lds, s>>>(a); break;
-        case 5: gemv_q_kernel<FMT, 5, WG><<<grid, WG, lds, s>>>(a); break;
-        case 6: gemv_q_kernel<FMT, 6, WG><<<grid, WG, lds, s>>>(a); break;
-        case 7: gemv_q_kernel<FMT, 7, WG><<<grid, WG, lds, s>>>(a); break;
-        default: gemv_q_kernel<FMT, 8, WG><<<grid, WG, lds, s>>>(a); break;
+        case 1: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 1, WG>);
+        case 2: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 2, WG>);
+        case 3: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 3, WG>);
+        case 4: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 4, WG>);
+        case 5: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 5, WG>);
+        case 6: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 6, WG>);
+        case 7: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 7, WG>);
+        default: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 8, WG>);
     }
 }
 
@@ -214,38 +274,56 @@ static int env_int(const char* name, int dflt) {
     return e ? atoi(e) : dflt;
 }
 
+// Resident workgroups per CU of one kernel instance (register and LDS
+// limited), cached per (kernel, LDS bytes).
+static int resident_per_cu(const void* fn, int wg, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, size_t>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto key = std::make_pair(fn, lds);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, wg, lds) != hipSuccess || nb <= 0) nb = 1;
+    cache[key] = nb;
+    return nb;
+}
+
 hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStream_t s) {
     if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
     GemvArgs a = a_in;
     // Tuning knobs (defaults measured on MI355X): MMHIP_GEMV_WG threads per
     // workgroup (256 | 512), MMHIP_GEMV_MAX_UPS caps record units per step,
-    // MMHIP_GEMV_WG_PER_CU the workgroups per CU the grid aims for.
-    static const int wg = env_int("MMHIP_GEMV_WG", 256) == 512 ? 512 : 256;
+    // MMHIP_GEMV_WG_PER_CU overrides the resident workgroups per CU that the
+    // grid is sized for (default: the occupancy the kernel reaches).
+    static const int wg_env = env_int("MMHIP_GEMV_WG", 256);
+    static const int wg = (wg_env == 512 || wg_env == 768) ? wg_env : 256;
     static const int cap_env = env_int("MMHIP_GEMV_MAX_UPS", 0);
-    // IQ2_XXS steps above 4 units exceed 128 VGPRs (4 waves per SIMD) and spill.
-    const int cap = cap_env > 0 ? cap_env : (fmt == kFmtIq2 ? 4 : 8);
-    static const int wg_per_cu = env_int("MMHIP_GEMV_WG_PER_CU", 4);
+    // Steps above 4 units exceed the register budget of 3 waves per SIMD
+    // (168 VGPRs with two record buffers) and spill.
+    const int cap = cap_env > 0 ? cap_env : 4;
+    static const int wg_per_cu_env = env_int("MMHIP_GEMV_WG_PER_CU", 0);
+    int ups = pick_ups(fmt, a.units);
+    if (ups == 0) return hipErrorInvalidValue;
+    while (ups > cap && ups % 2 == 0 && (fmt == kFmtIq2 || ups > 4)) ups /= 2;
+    const void* fn = fmt == kFmtIq2
+                         ? (wg == 768 ? kernel_for<kFmtIq2, 768>(ups)
+                                      : wg == 512 ? kernel_for<kFmtIq2, 512>(ups) : kernel_for<kFmtIq2, 256>(ups))
+                         : (wg == 768 ? kernel_for<kFmtQ8, 768>(ups)
+                                      : wg == 512 ? kernel_for<kFmtQ8, 512>(ups) : kernel_for<kFmtQ8, 256>(ups));
+    const size_t lds = gemv_q_lds_bytes(fmt, a.units);
+    const int wg_per_cu = wg_per_cu_env > 0 ? wg_per_cu_env : resident_per_cu(fn, wg, lds);
     const uint32_t waves = wg / 64;
     const uint64_t total_tiles = (uint64_t)a.n_probs * a.tiles;
-    const uint64_t target_wgs = (uint64_t)(num_cu > 0 ? num_cu : 256) * (wg_per_cu > 0 ? wg_per_cu : 4);
+    const uint64_t target_wgs = (uint64_t)(num_cu > 0 ? num_cu : 256) * wg_per_cu;
     uint64_t tpw = (total_tiles + target_wgs - 1) / target_wgs;  // tiles per WG
     tpw = (tpw + waves - 1) / waves * waves;
     if (tpw < waves) tpw = waves;
     if (tpw > a.tiles) tpw = (a.tiles + waves - 1) / waves * waves;
     a.tiles_per_wg = (uint32_t)tpw;
     dim3 grid((unsigned)((a.tiles + tpw - 1) / tpw), a.n_probs);
-    const size_t lds = gemv_q_lds_bytes(fmt, a.units);
-    int ups = pick_ups(fmt, a.units);
-    if (ups == 0) return hipErrorInvalidValue;
-    while (ups > cap && ups % 2 == 0 && (fmt == kFmtIq2 || ups > 4)) ups /= 2;
-    if (fmt == kFmtIq2) {
-        if (wg == 512) launch_ups<kFmtIq2, 512>(ups, grid, lds, s, a);
-        else launch_ups<kFmtIq2, 256>(ups, grid, lds, s, a);
-    } else {
-        if (wg == 512) launch_ups<kFmtQ8, 512>(ups, grid, lds, s, a);
-        else launch_ups<kFmtQ8, 256>(ups, grid, lds, s, a);
-    }
-    return hipGetLastError();
+    void* args[] = {&a};
+    return hipLaunchKernel(fn, grid, dim3(wg), args, lds, s);
 }
 
 hipError_t launch_gemv_float(const void* w, uint32_t type, uint64_t mat_stride, const float* x,

@@ -35,7 +35,7 @@ template <int FMT>
 __global__ __launch_bounds__(kQmmThreads) void qmm_kernel(QmmArgs a) {
     __shared__ uint32_t tab[FMT == kFmtIq2 ? kIq2TableWords : 4];
     if (FMT == kFmtIq2) {
-        load_iq2_tables(tab, a.tables);
+        build_iq2_tables<kQmmThreads>(tab, iq2_grid_entry());
         __syncthreads();
     }
     const uint32_t lane = threadIdx.x & 63;

@@ -33,6 +33,14 @@ __device__ __forceinline__ void iq2_decode_unit(const uint4& rr, const uint32_t*
     for (int s = 0; s < 8; ++s) b[s] = (s & 1) ? iq2_bop_hi(w4[s >> 1], tab) : iq2_bop_lo(w4[s >> 1], tab);
 }
 
+// f16 scale bits of unit i of a decode step: steps of 2, 4 or 8 units load
+// their scales packed two per dword, other step sizes one per word.
+template <int UPS>
+__device__ __forceinline__ uint32_t iq2_scale_bits(const uint32_t (&dw)[kMaxUnitsPerStep], int i) {
+    if (UPS == 2 || UPS == 4 || UPS == 8) return (dw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+    return dw[i];
+}
+
 // One decode step of UPS record units (compile-time, fully unrolled).
 // IQ2_XXS: unit i is 256-column group ub + i of the LDS activation chunk.
 // Only lanes n = 0, 1 (A rows 0 / 1) carry activation digits; the other
@@ -62,7 +70,7 @@ __device__ __forceinline__ void step_dot_iq2(const uint4 (&r)[kMaxUnitsPerStep],
         }
         const int w0 = gather_rows4(v[0], v[1], v[2], v[3]);
         const int w1 = gather_rows4(v[4], v[5], v[6], v[7]);
-        const float dq = f16_scale(dw[i]) * 0.25f;
+        const float dq = f16_scale(iq2_scale_bits<UPS>(dw, i)) * 0.25f;
         const float hdq = dq * 0.5f;
         const float c0 = fmaf((float)iq2_ls_a(r[i]), dq, hdq) * xs_g[blk0];
         const float c1 = fmaf((float)iq2_ls_b(r[i]), dq, hdq) * xs_g[blk0 + 4];
