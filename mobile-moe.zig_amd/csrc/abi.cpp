@@ -99,16 +99,6 @@ int mmhip_init(mmhip_ctx** out_ctx, int device) {
         delete ctx;
         return hip_fail(e, "init: hipStreamCreate");
     }
-    uint32_t tables[kIq2TableWordsHost];
-    build_iq2_tables(tables);
-    e = hipMalloc(&ctx->iq2_tables, sizeof(tables));
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(ctx->iq2_tables, tables, sizeof(tables), hipMemcpyHostToDevice, ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) {
-        mmhip_destroy(ctx);
-        return hip_fail(e, "init: tables");
-    }
     *out_ctx = ctx;
     return MMHIP_OK;
 }
@@ -125,7 +115,6 @@ void mmhip_destroy(mmhip_ctx* ctx) {
     ctx->d_q.release();
     ctx->h_in.release();
     ctx->h_out.release();
-    if (ctx->iq2_tables) (void)hipFree(ctx->iq2_tables);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }

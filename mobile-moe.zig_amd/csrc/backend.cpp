@@ -106,43 +106,23 @@ size_t quant_act_bytes(uint64_t n_vec, uint64_t cols_pad) {
     return (size_t)(2 * n_vec * stride + n_vec * (stride / 32) * 4);
 }
 
-// Builds the IQ2_XXS LDS tables (layout in kernels/device_common.hpp):
-//   LO[idx * 16 + (b012 | P << 3)]       columns 0..3, sign bits b0 b1 b2 b3,
-//                                        b3 = P ^ parity(b012)
-//   HI[hi3 * 512 + idx * 2 + P]          columns 4..7, sign bits hi3 (4..6) and
-//                                        bit 7 = P ^ parity(hi3)
-// Each entry packs four signed int8 weights grid_byte * (+-1).
-void build_iq2_tables(uint32_t* out) {
-    static const uint64_t grid[256] = {
-#include "iq2xxs_grid.inc"
-    };
-    auto pack = [](uint64_t g, int first, uint32_t signs) {
-        uint32_t word = 0;
-        for (int j = 0; j < 4; ++j) {
-            int v = (int)((g >> (8 * (first + j))) & 0xFFu);
-            if ((signs >> j) & 1u) v = -v;
-            word |= (uint32_t)(uint8_t)(int8_t)v << (8 * j);
-        }
-        return word;
-    };
-    for (uint32_t idx = 0; idx < 256; ++idx) {
-        for (uint32_t e = 0; e < 16; ++e) {
-            const uint32_t b012 = e & 7u, p = e >> 3;
-            const uint32_t b3 = p ^ (uint32_t)(__builtin_popcount(b012) & 1);
-            out[idx * 16 + e] = pack(grid[idx], 0, b012 | (b3 << 3));
-        }
-        for (uint32_t hi3 = 0; hi3 < 8; ++hi3) {
-            for (uint32_t p = 0; p < 2; ++p) {
-                const uint32_t b7 = p ^ (uint32_t)(__builtin_popcount(hi3) & 1);
-                out[4096 + hi3 * 512 + idx * 2 + p] = pack(grid[idx], 4, hi3 | (b7 << 3));
-            }
-        }
-    }
-}
-
 int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t type, uint64_t rows,
                   uint64_t cols, uint64_t count, mmhip_weight** out) {
+    const WeightSegment seg{raw, count};
+    return weight_create_segments(ctx, &seg, 1, raw_on_device, type, rows, cols, out);
+}
+
+int weight_create_segments(mmhip_ctx* ctx, const WeightSegment* segs, size_t n_segs, bool raw_on_device,
+                           uint32_t type, uint64_t rows, uint64_t cols, mmhip_weight** out) {
     *out = nullptr;
+    uint64_t count = 0;
+    for (size_t i = 0; i < n_segs; ++i) {
+        if (!segs[i].raw && segs[i].count) {
+            set_error(MMHIP_ERR_INVALID, "weight: null source");
+            return MMHIP_ERR_INVALID;
+        }
+        count += segs[i].count;
+    }
     if (rows == 0 || cols == 0 || count == 0) {
         set_error(MMHIP_ERR_INVALID, "weight: rows, cols and count must be > 0");
         return MMHIP_ERR_INVALID;
@@ -157,7 +137,22 @@ int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t 
         return MMHIP_ERR_INVALID;
     }
     const uint64_t row_bytes = ((cols + block_size(type) - 1) / block_size(type)) * block_bytes(type);
-    const uint64_t raw_bytes = row_bytes * rows * count;
+    const uint64_t mat_bytes = row_bytes * rows;
+    const uint64_t raw_bytes = mat_bytes * count;
+    // Copies every segment to dst (device) back to back.
+    auto gather = [&](char* dst) -> hipError_t {
+        uint64_t off = 0;
+        for (size_t i = 0; i < n_segs; ++i) {
+            const uint64_t b = segs[i].count * mat_bytes;
+            if (!b) continue;
+            hipError_t e = hipMemcpyAsync(dst + off, segs[i].raw, b,
+                                          raw_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                          ctx->stream);
+            if (e != hipSuccess) return e;
+            off += b;
+        }
+        return hipSuccess;
+    };
     mmhip_weight* w = new mmhip_weight();
     w->type = type;
     w->rows = rows;
@@ -171,8 +166,7 @@ int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t 
             return hip_fail(e, "weight: hipMalloc");
         }
         w->bytes = raw_bytes;
-        e = hipMemcpyAsync(w->plain, raw, raw_bytes, raw_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
-                           ctx->stream);
+        e = gather(static_cast<char*>(w->plain));
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) {
             weight_destroy(w);
@@ -210,11 +204,10 @@ int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t 
         weight_destroy(w);
         return hip_fail(e, "weight: memset");
     }
-    const void* src = raw;
-    if (!raw_on_device) {
+    const void* src = segs[0].raw;
+    if (!raw_on_device || n_segs > 1) {
         e = ctx->d_raw.ensure(raw_bytes);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(ctx->d_raw.p, raw, raw_bytes, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = gather(static_cast<char*>(ctx->d_raw.p));
         if (e != hipSuccess) {
             weight_destroy(w);
             return hip_fail(e, "weight: upload");
@@ -270,7 +263,10 @@ int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t 
     a.x_stride = x_stride;
     a.y = y;
     a.y_stride = y_stride;
-    a.tables = ctx->iq2_tables;
+    a.probs = nullptr;
+    a.n_active = nullptr;
+    a.x2_off = 0;
+    a.silu_mul = 0;
     a.first_mat = first;
     a.n_probs = (uint32_t)n;
     a.tiles = (uint32_t)g.tiles;
@@ -316,8 +312,7 @@ int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float*
     const uint64_t ld = out_layout == 0 ? w->rows : batch;
     {
         TimedLaunch tl(ctx, "qmm");
-        e = launch_qmm(w->recs, w->dvals, g, mat, q, (uint32_t)batch, y, ld, out_layout, ctx->iq2_tables,
-                       ctx->stream);
+        e = launch_qmm(w->recs, w->dvals, g, mat, q, (uint32_t)batch, y, ld, out_layout, ctx->stream);
     }
     return e == hipSuccess ? MMHIP_OK : hip_fail(e, "qmm: launch");
 }

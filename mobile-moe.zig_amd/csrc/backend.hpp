@@ -76,7 +76,6 @@ struct mmhip_ctx {
     int device = 0;
     int num_cu = 0;
     hipStream_t stream = nullptr;
-    uint32_t* iq2_tables = nullptr;  // 32 KiB, device
     std::mutex mu;                   // seam calls: scratch + residency map
     std::map<std::tuple<const void*, uint32_t, uint64_t, uint64_t>, mmhip_weight*> resident;
     mmhip::DevBuf d_in, d_out, d_raw, d_q;
@@ -102,6 +101,13 @@ namespace mmhip {
 // Upload helpers shared by the ABI and the MoE layer.
 int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t type, uint64_t rows,
                   uint64_t cols, uint64_t count, mmhip_weight** out);
+// One stacked weight from several sources of `count` matrices each, in order.
+struct WeightSegment {
+    const void* raw;
+    uint64_t count;
+};
+int weight_create_segments(mmhip_ctx* ctx, const WeightSegment* segs, size_t n_segs, bool raw_on_device,
+                           uint32_t type, uint64_t rows, uint64_t cols, mmhip_weight** out);
 void weight_destroy(mmhip_weight* w);
 
 // Layout of quantised activations inside one scratch allocation.

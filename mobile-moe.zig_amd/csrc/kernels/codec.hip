@@ -153,6 +153,31 @@ __global__ void quantize_kernel(const float* __restrict__ x, uint64_t x_stride, 
     if (j == 0) sc[v * s_stride + b] = s;
 }
 
+// silu(g) * u per row, then as quantize_kernel; rows r >= *n_rows are skipped.
+__global__ void quantize_silu_kernel(const float* __restrict__ src, uint64_t src_stride, uint64_t u_off,
+                                     const uint32_t* __restrict__ n_rows, uint32_t n_max, uint32_t cols,
+                                     uint32_t cols_pad, int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                     float* __restrict__ sc, uint64_t q_stride, uint64_t s_stride) {
+    const uint32_t nblk = cols_pad / 32;
+    const uint64_t blk = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+    const uint32_t j = threadIdx.x & 31;
+    const uint32_t rows = n_rows ? min(*n_rows, n_max) : n_max;
+    if (blk >= (uint64_t)rows * nblk) return;  // whole 32-lane group exits together
+    const uint64_t v = blk / nblk;
+    const uint32_t b = (uint32_t)(blk % nblk);
+    const uint32_t col = b * 32 + j;
+    float xv = 0.0f;
+    if (col < cols) {
+        const float* g = src + v * src_stride;
+        xv = silu(g[col]) * g[u_off + col];
+    }
+    int8_t h, l;
+    const float s = quantize_block32(xv, &h, &l);
+    hi[v * q_stride + col] = h;
+    lo[v * q_stride + col] = l;
+    if (j == 0) sc[v * s_stride + b] = s;
+}
+
 }  // namespace
 
 hipError_t launch_dequant(const void* raw, uint32_t type, uint64_t n, float* out, hipStream_t s) {
@@ -201,6 +226,17 @@ hipError_t launch_quantize(const float* x, uint64_t x_stride, uint32_t n_vec, ui
     const int bs = 256;
     quantize_kernel<<<(unsigned)((threads + bs - 1) / bs), bs, 0, s>>>(
         x, x_stride, n_vec, cols, cols_pad, q.hi, q.lo, q.scale, q.stride, q.scale_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_silu(const float* src, uint64_t src_stride, uint64_t u_off, const uint32_t* n_rows,
+                                uint32_t n_rows_max, uint32_t cols, uint32_t cols_pad, const QuantAct& q,
+                                hipStream_t s) {
+    const uint64_t threads = (uint64_t)n_rows_max * cols_pad;
+    if (threads == 0) return hipSuccess;
+    const int bs = 256;
+    quantize_silu_kernel<<<(unsigned)((threads + bs - 1) / bs), bs, 0, s>>>(
+        src, src_stride, u_off, n_rows, n_rows_max, cols, cols_pad, q.hi, q.lo, q.scale, q.stride, q.scale_stride);
     return hipGetLastError();
 }
 

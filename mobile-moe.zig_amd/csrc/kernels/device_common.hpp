@@ -186,9 +186,9 @@ __device__ __forceinline__ uint32_t negate_bytes(uint32_t w, uint32_t mask) {
 }
 
 // Builds the 32 KiB sign/grid tables (layout above) in LDS from the 2 KiB
-// grid, for blocks of 256, 512 or 768 threads: thread t handles grid index
+// grid, for blocks of 256 or 512 threads: thread t handles grid index
 // t % 256; with 256 threads it writes LO[idx * 16 .. +15] and the 16 HI words
-// of idx, with more threads threads 0..255 write LO, 256..511 HI.
+// of idx, with 512 threads the first half writes LO and the second half HI.
 // iq2_grid_entry issues the thread's grid load (put it ahead of the kernel's
 // bulk loads: waits on vector loads complete in issue order);
 // build_iq2_tables writes the tables. The caller synchronises before the
@@ -197,7 +197,7 @@ __device__ __forceinline__ uint64_t iq2_grid_entry() { return c_iq2_grid[threadI
 
 template <int WG>
 __device__ __forceinline__ void build_iq2_tables(uint32_t* tab, uint64_t gv) {
-    static_assert(WG == 256 || WG == 512 || WG == 768, "table build assumes 256, 512 or 768 threads");
+    static_assert(WG == 256 || WG == 512, "table build assumes 256 or 512 threads");
     const uint32_t idx = threadIdx.x & 255u;
     if (WG == 256 || threadIdx.x < 256) {
         const uint32_t lo = (uint32_t)gv;
@@ -211,7 +211,7 @@ __device__ __forceinline__ void build_iq2_tables(uint32_t* tab, uint64_t gv) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) d[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
     }
-    if (WG == 256 || (threadIdx.x >= 256 && threadIdx.x < 512)) {
+    if (WG == 256 || threadIdx.x >= 256) {
         const uint32_t hi = (uint32_t)(gv >> 32);
 #pragma unroll
         for (uint32_t h3 = 0; h3 < 8; ++h3) {
@@ -318,6 +318,15 @@ __device__ __forceinline__ void x_pass_load(BufRsrc xr, uint32_t b0, float (&v)[
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(buf_load_b32(xr, off + 4 * e, 0));
 }
+// silu(x) = x / (1 + exp(-x))  (math.zig:38-41).
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// v = silu(v) * u elementwise (expertFFN's siluInplace + mul, inference.zig:1179-1180).
+__device__ __forceinline__ void silu_mul4(float (&v)[4], const float (&u)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = silu(v[e]) * u[e];
+}
+
 __device__ __forceinline__ void x_pass_store(const float (&v)[4], uint32_t nblk, uint32_t b0, int8_t* aq, float* xs) {
     uint32_t h4, l4;
     const float s = quantize_quad(v, h4, l4);
@@ -329,12 +338,16 @@ __device__ __forceinline__ void x_pass_store(const float (&v)[4], uint32_t nblk,
         if (jq == 0) xs[b] = s;
     }
 }
-// Whole activation chunk: blocks [0, nblk) of the vector behind xr.
+// Whole activation chunk: blocks [0, nblk) of the vector behind xr (times
+// silu: silu(x) * u with u behind ur).
 template <int WG>
-__device__ __forceinline__ void quantize_to_lds(BufRsrc xr, uint32_t nblk, int8_t* aq, float* xs) {
+__device__ __forceinline__ void quantize_to_lds(BufRsrc xr, BufRsrc ur, bool silu_mul, uint32_t nblk, int8_t* aq,
+                                                float* xs) {
     for (uint32_t b0 = 0; b0 < nblk; b0 += WG / 8) {
-        float v[4];
+        float v[4], u[4];
         x_pass_load(xr, b0, v);
+        x_pass_load(ur, b0, u);
+        if (silu_mul) silu_mul4(v, u);
         x_pass_store(v, nblk, b0, aq, xs);
     }
 }

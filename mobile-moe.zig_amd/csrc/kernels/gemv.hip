@@ -79,7 +79,7 @@ __device__ __forceinline__ void load_step(BufRsrc rr, uint32_t rec_voff, uint32_
 // A ring of three register buffers keeps the next two steps' loads in flight
 // while a step computes.
 template <int FMT, int UPS, int WG>
-__global__ __launch_bounds__(WG, (WG == 256 ? 3 : WG == 512 ? 2 : 1)) void gemv_q_kernel(GemvArgs a) {
+__global__ __launch_bounds__(WG, (WG == 256 ? 3 : 2)) void gemv_q_kernel(GemvArgs a) {
     constexpr uint32_t kWaves = WG / 64;
     // Static LDS for the tables (known address: table offsets fold into the
     // ds_read immediates); dynamic LDS for the activation chunk.
@@ -96,8 +96,17 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 3 : WG == 512 ? 2 : 1)) void gemv_
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t p = blockIdx.y;
-    const uint64_t mat = a.first_mat + p;
-    const float* x = a.x + (uint64_t)p * a.x_stride;
+    if (a.n_active && p >= *a.n_active) return;  // whole workgroup: problem not in this call's list
+    uint64_t mat = a.first_mat + p, x_row = p, y_row = p;
+    if (a.probs) {
+        const uint4 d = a.probs[p];
+        mat = d.x;
+        x_row = d.y;
+        y_row = d.z;
+    }
+    const float* x = a.x + x_row * a.x_stride;
+    float* const y_base = a.y + y_row * a.y_stride;
+    const bool silu_mul = a.silu_mul != 0;
     const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
     // this wave's tiles: t_begin + wave + kWaves * i, i < my_n
     uint32_t my_n = 0;
@@ -145,7 +154,7 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 3 : WG == 512 ? 2 : 1)) void gemv_
             acc = 0.0f;
             const uint32_t row = tile_of(s) * 16 + n;
             if (lane < 16 && row < a.rows) {
-                float* yp = a.y + (uint64_t)p * a.y_stride + row;
+                float* yp = y_base + row;
                 *yp = (kb == 0) ? tot : *yp + tot;
             }
         }
@@ -155,12 +164,16 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 3 : WG == 512 ? 2 : 1)) void gemv_
         // Prologue of the first chunk (two activation passes cover 32 * WG / 4
         // columns; longer chunks quantise the rest after the weight loads).
         const uint32_t nb = chunk_blk;
-        const BufRsrc x_r = make_rsrc(x, min(a.cols, chunk_blk * 32) * 4);
+        const uint32_t xb = min(a.cols, chunk_blk * 32) * 4;
+        const BufRsrc x_r = make_rsrc(x, xb);
+        const BufRsrc u_r = make_rsrc(x + a.x2_off, silu_mul ? xb : 0);  // zero-size: loads read 0
         uint64_t gv = 0;
         if (FMT == kFmtIq2) gv = iq2_grid_entry();
-        float xv0[4], xv1[4];
+        float xv0[4], xv1[4], uv0[4], uv1[4];
         x_pass_load(x_r, 0, xv0);
         x_pass_load(x_r, WG / 8, xv1);
+        x_pass_load(u_r, 0, uv0);
+        x_pass_load(u_r, WG / 8, uv1);
         // A CU serves its waves' loads in issue order: the barrier (no memory
         // fence, no wait) puts every wave's small loads ahead of the weights.
         __builtin_amdgcn_s_barrier();
@@ -168,11 +181,17 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 3 : WG == 512 ? 2 : 1)) void gemv_
         load(1, r1, d1);
         load(2, r2, d2);
         if (FMT == kFmtIq2) build_iq2_tables<WG>(tab, gv);
+        if (silu_mul) {
+            silu_mul4(xv0, uv0);
+            silu_mul4(xv1, uv1);
+        }
         x_pass_store(xv0, nb, 0, aq, xs);
         x_pass_store(xv1, nb, WG / 8, aq, xs);
         for (uint32_t b0 = 2 * (WG / 8); b0 < nb; b0 += WG / 8) {
-            float v[4];
+            float v[4], u[4];
             x_pass_load(x_r, b0, v);
+            x_pass_load(u_r, b0, u);
+            if (silu_mul) silu_mul4(v, u);
             x_pass_store(v, nb, b0, aq, xs);
         }
     }
@@ -198,7 +217,9 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 3 : WG == 512 ? 2 : 1)) void gemv_
         load(1, r1, d1);
         load(2, r2, d2);
         const uint32_t c0 = kb * 32;
-        quantize_to_lds<WG>(make_rsrc(x + c0, (a.cols > c0 ? min(a.cols - c0, nb * 32) : 0) * 4), nb, aq, xs);
+        const uint32_t cb = (a.cols > c0 ? min(a.cols - c0, nb * 32) : 0) * 4;
+        quantize_to_lds<WG>(make_rsrc(x + c0, cb), make_rsrc(x + a.x2_off + c0, silu_mul ? cb : 0), silu_mul, nb, aq,
+                            xs);
     }
 }
 
@@ -296,8 +317,7 @@ hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStre
     // workgroup (256 | 512), MMHIP_GEMV_MAX_UPS caps record units per step,
     // MMHIP_GEMV_WG_PER_CU overrides the resident workgroups per CU that the
     // grid is sized for (default: the occupancy the kernel reaches).
-    static const int wg_env = env_int("MMHIP_GEMV_WG", 256);
-    static const int wg = (wg_env == 512 || wg_env == 768) ? wg_env : 256;
+    static const int wg = env_int("MMHIP_GEMV_WG", 256) == 512 ? 512 : 256;
     static const int cap_env = env_int("MMHIP_GEMV_MAX_UPS", 0);
     // Steps above 4 units exceed the register budget of 3 waves per SIMD
     // (168 VGPRs with two record buffers) and spill.
@@ -306,11 +326,8 @@ hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStre
     int ups = pick_ups(fmt, a.units);
     if (ups == 0) return hipErrorInvalidValue;
     while (ups > cap && ups % 2 == 0 && (fmt == kFmtIq2 || ups > 4)) ups /= 2;
-    const void* fn = fmt == kFmtIq2
-                         ? (wg == 768 ? kernel_for<kFmtIq2, 768>(ups)
-                                      : wg == 512 ? kernel_for<kFmtIq2, 512>(ups) : kernel_for<kFmtIq2, 256>(ups))
-                         : (wg == 768 ? kernel_for<kFmtQ8, 768>(ups)
-                                      : wg == 512 ? kernel_for<kFmtQ8, 512>(ups) : kernel_for<kFmtQ8, 256>(ups));
+    const void* fn = fmt == kFmtIq2 ? (wg == 512 ? kernel_for<kFmtIq2, 512>(ups) : kernel_for<kFmtIq2, 256>(ups))
+                                    : (wg == 512 ? kernel_for<kFmtQ8, 512>(ups) : kernel_for<kFmtQ8, 256>(ups));
     const size_t lds = gemv_q_lds_bytes(fmt, a.units);
     const int wg_per_cu = wg_per_cu_env > 0 ? wg_per_cu_env : resident_per_cu(fn, wg, lds);
     const uint32_t waves = wg / 64;

@@ -10,8 +10,6 @@ namespace mmhip {
 
 enum TileFormat : uint32_t { kFmtQ8 = 0, kFmtIq2 = 1 };
 
-constexpr int kIq2TableWordsHost = 8192;  // u32 words of the IQ2_XXS LDS tables
-
 // Geometry of a stacked weight in the tile layout (device_common.hpp).
 struct TileGeom {
     uint32_t fmt;
@@ -41,13 +39,23 @@ struct GemvArgs {
     uint32_t d_row;
     const float* x;                 // f32 activations, quantised inside the kernel
     uint64_t x_stride;              // floats between problems' vectors; 0 = shared
+    uint64_t x2_off;                // silu_mul: floats from a problem's x to its second vector
+    uint32_t silu_mul;              // 1: the activation is silu(x) * x2 (expertFFN, inference.zig:1179-1180)
     float* y;
     uint64_t y_stride;
-    const uint32_t* tables;         // IQ2_XXS LDS tables (32 KiB)
     uint64_t first_mat;
+    const uint4* probs;             // device [n_probs] {matrix, x row, y row, 0}, or null: (first_mat + p, p, p)
+    const uint32_t* n_active;       // device: problems p >= *n_active do nothing, or null
     uint32_t n_probs, tiles, units, rows, cols;
     uint32_t tiles_per_wg;          // set by launch_gemv_q
 };
+
+// One item of a grouped (expert-sorted) QMM: rows [slot, slot + count) of the
+// activation list against matrix `mat`; count <= kQmmTokens.
+struct QmmWork {
+    uint32_t mat, slot, count, pad;
+};
+constexpr uint32_t kQmmTokens = 32;  // activation rows per QMM wave
 
 // Raw GGUF bytes -> f32, bit-exact (dequant.zig:316-390, 632-659).
 hipError_t launch_dequant(const void* raw, uint32_t ggml_type, uint64_t n, float* out, hipStream_t s);
@@ -74,9 +82,64 @@ hipError_t launch_gemv_float(const void* w, uint32_t ggml_type, uint64_t mat_str
 // out_layout 0: y[b * y_ld + r]; 1: y[r * y_ld + b].
 hipError_t launch_qmm(const uint4* recs, const uint16_t* dvals, const TileGeom& g, uint64_t mat,
                       const QuantAct& xq, uint32_t batch, float* y, uint64_t y_ld, int out_layout,
-                      const uint32_t* tables, hipStream_t s);
+                      hipStream_t s);
 
-// Builds the two IQ2_XXS LDS tables on the host (8192 u32).
-void build_iq2_tables(uint32_t* out8192);
+// Grouped QMM: work item i < *n_work multiplies activation rows
+// a_row[slot .. slot + count) (a_row null: the slots themselves) by matrix
+// work[i].mat and writes y[(slot + j) * y_ld + r]. max_work bounds the grid.
+hipError_t launch_qmm_grouped(const uint4* recs, const uint16_t* dvals, const TileGeom& g, const QuantAct& xq,
+                              const uint32_t* a_row, const QmmWork* work, const uint32_t* n_work,
+                              uint32_t max_work, float* y, uint64_t y_ld, hipStream_t s);
+
+// Quantises silu(g) * u per row (rows r < *n_rows, or n_rows_max when
+// n_rows is null): g = src + r * src_stride, u = g + u_off.
+hipError_t launch_quantize_silu(const float* src, uint64_t src_stride, uint64_t u_off, const uint32_t* n_rows,
+                                uint32_t n_rows_max, uint32_t cols, uint32_t cols_pad, const QuantAct& q,
+                                hipStream_t s);
+
+// ---- MoE routing and combine (moe.hip) ----
+//
+// Activation slots of one MoE call over T tokens: routed (token, expert)
+// pairs occupy slots [0, 4T) (T == 1: route order; T > 1: sorted by expert,
+// tokens in order), the shared expert of token t is slot 4T + t. Gate/up
+// outputs are rows of 2 * inter floats per slot (gate, then up), expert
+// outputs rows of hidden floats.
+
+// Scheduler.route (scheduler.zig:169-262) for every token on the device, plus
+// the problem lists of the expert products.
+struct RouteArgs {
+    const float* scores;        // [n_tokens][n_experts]
+    uint32_t n_tokens, n_experts;
+    uint32_t k;                 // min(active_expert_limit, 4), >= 1
+    int32_t level;              // throttle level 0..3
+    float scale;                // getRoutedScalingFactor
+    uint32_t shared;            // 1: the layer has a shared expert
+    uint32_t shared_merged;     // 1: shared gate/up are matrices 2E, 2E+1 and shared down is matrix E
+    unsigned long long* counts; // ExpertStats.counts of the layer [n_experts]
+    uint32_t* route_ids;        // [n_tokens][4] or null
+    float* route_w;             // [n_tokens][4] or null
+    int32_t* assign_slot;       // [n_tokens][4]: slot of (t, i), -1 = none (skipped or i >= k)
+    float* assign_w;            // [n_tokens][4]
+    int32_t* shared_slot;       // [n_tokens]: slot of the shared expert, -1 = none
+    uint32_t* deferred;         // [n_tokens]
+    uint32_t* slot_tok;         // [5 n_tokens]: token of each slot
+    uint4* gemv_gu;             // n_tokens == 1: {matrix, 0, 2 slot + (0 gate | 1 up), 0}
+    uint4* gemv_dn;             //                {matrix, slot, slot, 0}
+    uint32_t* n_gemv;           // [2]: active entries of gemv_gu, gemv_dn
+    QmmWork* work_gu;           // n_tokens > 1: grouped items (gate col 0, up col inter)
+    QmmWork* work_dn;
+    uint32_t* n_work;           // [2]: active items of work_gu, work_dn
+    uint32_t inter;             // routed expert width (up column offset)
+};
+hipError_t launch_route(const RouteArgs& a, hipStream_t s);
+// Upper bound of the grouped items per list for T tokens and E experts.
+uint32_t route_max_work(uint32_t n_tokens, uint32_t n_experts);
+
+// out[t] = sum over the token's routed slots, in route order, of w * eo[slot]
+// (products and sums rounded separately), + eo[shared slot], + bias when
+// deferred  (moeFFN, inference.zig:977-1006).
+hipError_t launch_combine(const float* eo, const int32_t* assign_slot, const float* assign_w,
+                          const int32_t* shared_slot, const uint32_t* deferred, const float* bias, float* out,
+                          uint32_t n_tokens, uint32_t hidden, hipStream_t s);
 
 }  // namespace mmhip

@@ -1,0 +1,246 @@
+"""MoE FFN layer on the GPU against the oracle's moeFFN (inference.zig:886-1010).
+
+Routing ids must equal the oracle's; the only allowed exception is a token
+whose k-th and (k+1)-th router logits differ by less than 1e-5 relative, where
+the CPU path's own f32 reduction order decides (the GPU router sums in a
+different order). No seeded case here comes near that margin; the check is
+there so that a future change of inputs cannot turn a tie into a false alarm.
+Route weights: 1e-6 relative (expf on the GPU vs libm). Outputs: max-abs-rel
+1e-3 (f32 accumulation of block-quantised products, as the GEMV tests).
+"""
+import numpy as np
+import pytest
+
+import mmhip as mm
+
+pytestmark = pytest.mark.gpu
+
+TOL_OUT = 1e-3
+TOL_W = 1e-6
+TIE = 1e-5
+
+
+def _weights(rng, fmt, hidden, inter, n_exp, shared_inter=None, shared_fmt=None, router_sigma=0.02):
+    router = rng.normal(0.0, router_sigma, (n_exp, hidden)).astype(np.float32)
+    gate = mm.make_weight(rng, fmt, inter, hidden, n_exp)
+    up = mm.make_weight(rng, fmt, inter, hidden, n_exp)
+    down = mm.make_weight(rng, fmt, hidden, inter, n_exp)
+    shared = None
+    if shared_inter:
+        sf = shared_fmt if shared_fmt is not None else fmt
+        shared = (mm.make_weight(rng, sf, shared_inter, hidden), mm.make_weight(rng, sf, shared_inter, hidden),
+                  mm.make_weight(rng, sf, hidden, shared_inter))
+    return router, gate, up, down, shared
+
+
+def _layers(ctx, orc, fmt, hidden, inter, n_exp, router, gate, up, down, shared, shared_inter=None,
+            shared_fmt=None, rsf=1.0, bias=None):
+    kw = dict(hidden=hidden, inter=inter, n_experts=n_exp, expert_type=fmt, router=router, gate=gate, up=up,
+              down=down, shared=shared, shared_inter=shared_inter, shared_type=shared_fmt,
+              routed_scaling_factor=rsf)
+    gpu = mm.MoeLayer(ctx, **kw)
+    cpu = orc.Moe(deferral_bias=bias, **kw)
+    return gpu, cpu
+
+
+def _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c):
+    """Exact ids (tie rule above), weights to TOL_W, outputs to TOL_OUT."""
+    assert ids_g.shape == ids_c.shape
+    k = ids_c.shape[1]
+    logits = h.astype(np.float64) @ router.astype(np.float64).T
+    ok = np.ones(h.shape[0], dtype=bool)
+    for t in range(h.shape[0]):
+        if not np.array_equal(ids_g[t], ids_c[t]):
+            srt = np.sort(logits[t])[::-1]
+            gap = abs(srt[k - 1] - srt[k]) / max(abs(srt[k - 1]), 1e-30)
+            assert gap < TIE, f"token {t}: ids {ids_g[t]} vs {ids_c[t]} with logit gap {gap:.3g}"
+            ok[t] = False
+    assert ok.any()
+    np.testing.assert_allclose(w_g[ok], w_c[ok], rtol=TOL_W, atol=1e-7)
+    err = mm.max_abs_rel(out_g[ok], out_c[ok])
+    assert err < TOL_OUT, f"max-abs-rel {err:.3g}"
+    return err
+
+
+@pytest.mark.parametrize("fmt", ["iq2", "q8"])
+def test_decode_glm_shape(ctx, orc, fmt):
+    """One token through a GLM-4.7-Flash-shaped layer: hidden 2048, expert width
+    1536, 64 routed experts top-4 plus a shared expert."""
+    f = mm.IQ2_XXS if fmt == "iq2" else mm.Q8_0
+    rng = np.random.default_rng(300 if fmt == "iq2" else 301)
+    H, I, E = 2048, 1536, 64
+    router, gate, up, down, shared = _weights(rng, f, H, I, E, shared_inter=I)
+    gpu, cpu = _layers(ctx, orc, f, H, I, E, router, gate, up, down, shared, shared_inter=I)
+    try:
+        h = rng.standard_normal((1, H)).astype(np.float32)
+        out_g, ids_g, w_g = gpu.ffn(h)
+        out_c, ids_c, w_c = cpu.ffn(h)
+        assert ids_g.shape == (1, 4)
+        _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+    finally:
+        gpu.free()
+
+
+def _zipf_hidden(rng, t, hidden, n_exp, s=1.1):
+    """Hidden states whose first n_exp coordinates are the router logits under
+    an identity router: N(0, 1) with +10 on 4 distinct experts per token drawn
+    from Zipf(s) over a seeded permutation of the experts."""
+    perm = rng.permutation(n_exp)
+    p = 1.0 / np.arange(1, n_exp + 1) ** s
+    p /= p.sum()
+    h = rng.standard_normal((t, hidden)).astype(np.float32)
+    for ti in range(t):
+        chosen = perm[rng.choice(n_exp, 4, replace=False, p=p)]
+        h[ti, chosen] += 10.0
+    router = np.zeros((n_exp, hidden), dtype=np.float32)
+    router[:, :n_exp] = np.eye(n_exp, dtype=np.float32)
+    return h, router
+
+
+def test_prefill_zipf_batch64(ctx, orc):
+    """64 tokens, skewed routing over 64 IQ2_XXS experts, grouped by expert."""
+    rng = np.random.default_rng(310)
+    H, I, E, T = 2048, 1536, 64, 64
+    h, router = _zipf_hidden(rng, T, H, E)
+    _, gate, up, down, shared = _weights(rng, mm.IQ2_XXS, H, I, E, shared_inter=I)
+    gpu, cpu = _layers(ctx, orc, mm.IQ2_XXS, H, I, E, router, gate, up, down, shared, shared_inter=I)
+    pool = orc.Pool(4)
+    try:
+        out_g, ids_g, w_g = gpu.ffn(h)
+        out_c, ids_c, w_c = cpu.ffn(h, pool=pool)
+        _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+        counts = np.bincount(ids_c.reshape(-1).astype(np.int64), minlength=E)
+        assert counts.max() > 8  # the routing is skewed: one group spans several QMM rows
+    finally:
+        pool.close()
+        gpu.free()
+
+
+SMALL = dict(H=512, I=256, E=16)
+
+
+def _small_case(ctx, orc, seed, fmt=mm.IQ2_XXS, shared_inter=256, shared_fmt=None, rsf=1.0, bias=None):
+    rng = np.random.default_rng(seed)
+    H, I, E = SMALL["H"], SMALL["I"], SMALL["E"]
+    router, gate, up, down, shared = _weights(rng, fmt, H, I, E, shared_inter=shared_inter, shared_fmt=shared_fmt,
+                                              router_sigma=0.05)
+    gpu, cpu = _layers(ctx, orc, fmt, H, I, E, router, gate, up, down, shared, shared_inter=shared_inter,
+                       shared_fmt=shared_fmt, rsf=rsf, bias=bias)
+    return rng, router, gpu, cpu
+
+
+@pytest.mark.parametrize("t", [1, 2, 3, 33, 64, 256])
+def test_token_counts(ctx, orc, t):
+    """Decode (1) and grouped prefill (2..256 = MMHIP_MOE_MAX_TOKENS) paths."""
+    rng, router, gpu, cpu = _small_case(ctx, orc, 320 + t)
+    try:
+        h = rng.standard_normal((t, SMALL["H"])).astype(np.float32)
+        out_g, ids_g, w_g = gpu.ffn(h)
+        out_c, ids_c, w_c = cpu.ffn(h)
+        _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+    finally:
+        gpu.free()
+
+
+@pytest.mark.parametrize("level", [0, 1, 2, 3])
+@pytest.mark.parametrize("t", [1, 9])
+def test_throttle_levels(ctx, orc, level, t):
+    """ThrottleState levels: k = 4, 3, 2, 1 and routed scale 1, .83, .67, .5."""
+    rng, router, gpu, cpu = _small_case(ctx, orc, 330 + level + 10 * t, rsf=1.5)
+    try:
+        h = rng.standard_normal((t, SMALL["H"])).astype(np.float32)
+        out_g, ids_g, w_g = gpu.ffn(h, level=level)
+        out_c, ids_c, w_c = cpu.ffn(h, level=level)
+        assert ids_g.shape[1] == [4, 3, 2, 1][level]
+        _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+    finally:
+        gpu.free()
+
+
+@pytest.mark.parametrize("t", [1, 5])
+def test_heavy_fallback_with_deferral_bias(ctx, orc, t):
+    """Heavy throttle with the expert limit raised to 4: only the top expert
+    runs, renormalised to the routed scale, and the deferral bias is added."""
+    bias = np.random.default_rng(77).normal(0, 0.1, SMALL["H"]).astype(np.float32)
+    rng, router, gpu, cpu = _small_case(ctx, orc, 340 + t, bias=bias)
+    try:
+        h = rng.standard_normal((t, SMALL["H"])).astype(np.float32)
+        out_g, ids_g, w_g = gpu.ffn(h, level=3, active_expert_limit=4, deferral_bias=bias)
+        out_c, ids_c, w_c = cpu.ffn(h, level=3, active_expert_limit=4)
+        assert ids_g.shape[1] == 4
+        _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+        np.testing.assert_allclose(w_g[:, 0], 0.5, rtol=1e-6)
+        # Without the bias the outputs differ by exactly that bias (within rounding).
+        out_nb, _, _ = gpu.ffn(h, level=3, active_expert_limit=4)
+        assert mm.max_abs_rel(out_g - out_nb, np.broadcast_to(bias, out_g.shape)) < 1e-4
+    finally:
+        gpu.free()
+
+
+@pytest.mark.parametrize("t", [1, 7])
+def test_q8_experts(ctx, orc, t):
+    rng, router, gpu, cpu = _small_case(ctx, orc, 350 + t, fmt=mm.Q8_0)
+    try:
+        h = rng.standard_normal((t, SMALL["H"])).astype(np.float32)
+        out_g, ids_g, w_g = gpu.ffn(h)
+        out_c, ids_c, w_c = cpu.ffn(h)
+        _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+    finally:
+        gpu.free()
+
+
+@pytest.mark.parametrize("t", [1, 6])
+@pytest.mark.parametrize("variant", ["wider", "other_type", "none"])
+def test_shared_expert_variants(ctx, orc, t, variant):
+    """Shared expert of another width or type (separate launches) or absent."""
+    shared_inter = {"wider": 512, "other_type": 256, "none": None}[variant]
+    shared_fmt = mm.Q8_0 if variant == "other_type" else None
+    rng, router, gpu, cpu = _small_case(ctx, orc, 360 + t, shared_inter=shared_inter, shared_fmt=shared_fmt)
+    try:
+        h = rng.standard_normal((t, SMALL["H"])).astype(np.float32)
+        out_g, ids_g, w_g = gpu.ffn(h)
+        out_c, ids_c, w_c = cpu.ffn(h)
+        _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+    finally:
+        gpu.free()
+
+
+def test_expert_counts_follow_stats(ctx, orc):
+    """ExpertStats.counts: every selected expert of every call (skipped ones
+    included), accumulated over calls."""
+    rng, router, gpu, cpu = _small_case(ctx, orc, 370)
+    stats = orc.Stats(1, SMALL["E"])
+    try:
+        for t, level in ((1, 0), (11, 0), (4, 2), (3, 3)):
+            h = rng.standard_normal((t, SMALL["H"])).astype(np.float32)
+            gpu.ffn(h, level=level)
+            cpu.ffn(h, level=level, stats=stats)
+        np.testing.assert_array_equal(gpu.expert_counts(), stats.counts[:SMALL["E"]])
+    finally:
+        gpu.free()
+
+
+def test_device_twin_matches_host_call(ctx, orc):
+    rng, router, gpu, cpu = _small_case(ctx, orc, 380)
+    try:
+        t = 12
+        h = rng.standard_normal((t, SMALL["H"])).astype(np.float32)
+        out_h, _, _ = gpu.ffn(h)
+        hd = mm.DeviceArray.from_numpy(ctx, h)
+        od = mm.DeviceArray(ctx, h.nbytes)
+        gpu.ffn_dev(hd, od, t)
+        ctx.synchronize()
+        assert np.array_equal(od.to_numpy(np.float32, h.size).reshape(h.shape), out_h)
+    finally:
+        gpu.free()
+
+
+def test_invalid_calls(ctx, orc):
+    rng, router, gpu, cpu = _small_case(ctx, orc, 390)
+    try:
+        with pytest.raises(mm.MmhipError):
+            gpu.ffn(np.zeros((0, SMALL["H"]), np.float32))
+        with pytest.raises(mm.MmhipError):
+            gpu.ffn(np.zeros((257, SMALL["H"]), np.float32))
+    finally:
+        gpu.free()
