@@ -8,8 +8,8 @@
 // lane, through a ring of three register buffers so the next two steps'
 // loads are in flight while the current one computes. Every weight byte is read exactly once.
 //
-// f32 / f16 weights (the router, matVecMulUnified's f32 branch): one wave
-// per output row.
+// f32 / f16 weights (the router, matVecMulUnified's f32 branch): one
+// workgroup per output row.
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "tile_ops.hpp"
@@ -223,27 +223,48 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 3 : 2)) void gemv_q_kernel(GemvArg
     }
 }
 
-// f32 / f16 weights: one wave per output row.
+// f32 / f16 weights: one 256-thread workgroup per output row. Each pass
+// covers 2048 columns (8 per thread) with all of a thread's loads in flight
+// together; out-of-range columns read as zero through the buffer resources.
+constexpr int kFloatThreads = 256;
 template <typename WT>
-__global__ __launch_bounds__(256) void gemv_float_kernel(const WT* __restrict__ w, uint64_t mat_stride,
-                                                         const float* __restrict__ x, uint64_t x_stride,
-                                                         float* __restrict__ y, uint64_t y_stride,
-                                                         uint32_t n_mats, uint32_t rows, uint32_t cols) {
-    const uint32_t lane = threadIdx.x & 63;
-    const uint64_t wid = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    if (wid >= (uint64_t)n_mats * rows) return;
-    const uint32_t m = (uint32_t)(wid / rows), r = (uint32_t)(wid % rows);
-    const WT* wr = w + m * mat_stride + (uint64_t)r * cols;
-    const float* xv = x + m * x_stride;
+__global__ __launch_bounds__(kFloatThreads) void gemv_float_kernel(const WT* __restrict__ w, uint64_t mat_stride,
+                                                                   const float* __restrict__ x, uint64_t x_stride,
+                                                                   float* __restrict__ y, uint64_t y_stride,
+                                                                   uint32_t rows, uint32_t cols) {
+    __shared__ float part[kFloatThreads / 64];
+    const uint32_t m = blockIdx.y, r = blockIdx.x;
+    const BufRsrc wr = make_rsrc(w + m * mat_stride + (uint64_t)r * cols, cols * (uint32_t)sizeof(WT));
+    const BufRsrc xr = make_rsrc(x + m * x_stride, cols * 4);
     float acc = 0.0f;
-    for (uint32_t c = lane; c < cols; c += 64) {
-        float wv;
-        if constexpr (sizeof(WT) == 2) wv = f16_bits_to_f32(wr[c]);
-        else wv = wr[c];
-        acc = fmaf(wv, xv[c], acc);
+    for (uint32_t c0 = 0; c0 < cols; c0 += kFloatThreads * 8) {
+        const uint32_t c = c0 + threadIdx.x * 4;
+        float wv[8], xv[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t cc = c + h * kFloatThreads * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[4 * h + e] = __uint_as_float(buf_load_b32(xr, (cc + e) * 4, 0));
+            if constexpr (sizeof(WT) == 2) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) wv[4 * h + e] = f16_bits_to_f32(buf_load_b16(wr, (cc + e) * 2, 0));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) wv[4 * h + e] = __uint_as_float(buf_load_b32(wr, (cc + e) * 4, 0));
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf(wv[e], xv[e], acc);
     }
     acc = wave_sum(acc);
-    if (lane == 0) y[m * y_stride + r] = acc;
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kFloatThreads / 64; ++i) t += part[i];
+        y[m * y_stride + r] = t;
+    }
 }
 
 }  // namespace
@@ -346,15 +367,14 @@ hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStre
 hipError_t launch_gemv_float(const void* w, uint32_t type, uint64_t mat_stride, const float* x,
                              uint64_t x_stride, float* y, uint64_t y_stride, uint32_t n_mats,
                              uint32_t rows, uint32_t cols, hipStream_t s) {
-    const uint64_t waves = (uint64_t)n_mats * rows;
-    if (waves == 0) return hipSuccess;
-    const unsigned blocks = (unsigned)((waves * 64 + 255) / 256);
+    if ((uint64_t)n_mats * rows == 0) return hipSuccess;
+    const dim3 grid(rows, n_mats);
     if (type == 0)
-        gemv_float_kernel<float><<<blocks, 256, 0, s>>>((const float*)w, mat_stride, x, x_stride, y, y_stride,
-                                                        n_mats, rows, cols);
+        gemv_float_kernel<float><<<grid, kFloatThreads, 0, s>>>((const float*)w, mat_stride, x, x_stride, y, y_stride,
+                                                               rows, cols);
     else
-        gemv_float_kernel<uint16_t><<<blocks, 256, 0, s>>>((const uint16_t*)w, mat_stride, x, x_stride, y,
-                                                           y_stride, n_mats, rows, cols);
+        gemv_float_kernel<uint16_t><<<grid, kFloatThreads, 0, s>>>((const uint16_t*)w, mat_stride, x, x_stride, y,
+                                                                  y_stride, rows, cols);
     return hipGetLastError();
 }
 

@@ -1,6 +1,6 @@
 // MoE routing and combine on gfx950 (moeFFN, inference.zig:886-1010).
 //
-// route_kernel: one workgroup, one thread per token. Each token runs
+// route_kernel: one workgroup, one wave per token. Each token runs
 // Scheduler.route exactly as the CPU path does (math.topK's size-k min-heap,
 // softmax over the selected logits, throttle scaling, the heavy-throttle
 // top-1 fallback) and counts its experts (ExpertStats.counts). The workgroup
@@ -19,73 +19,163 @@ namespace mmhip {
 
 namespace {
 
-constexpr int kRouteThreads = 256;  // >= MMHIP_MOE_MAX_TOKENS
+constexpr int kRouteThreads = 1024;  // 16 waves; one wave per token at a time
+constexpr int kMaxTokens = 256;      // MMHIP_MOE_MAX_TOKENS
+constexpr int kMaxExperts = 256;
 constexpr int kMaxK = 4;
 
-// math.siftDownMin (math.zig:177-193).
-__device__ void sift_down_min(uint32_t (&hi)[kMaxK], float (&hs)[kMaxK], uint32_t start, uint32_t end) {
-    uint32_t parent = start;
-    for (;;) {
-        const uint32_t left = parent * 2 + 1, right = left + 1;
-        uint32_t smallest = parent;
-        if (left < end && hs[left] < hs[smallest]) smallest = left;
-        if (right < end && hs[right] < hs[smallest]) smallest = right;
-        if (smallest == parent) break;
-        const uint32_t ti = hi[parent];
-        hi[parent] = hi[smallest];
-        hi[smallest] = ti;
-        const float ts = hs[parent];
-        hs[parent] = hs[smallest];
-        hs[smallest] = ts;
-        parent = smallest;
+// The size-k min-heap of math.topK (math.zig:130-193) for k <= 4, held in
+// registers: every position is a compile-time index, so siftDownMin's
+// comparisons (children 2p+1, 2p+2 of parent p, strict <, left first) are
+// spelled out for the only parents a heap of <= 4 entries has: 0 and 1.
+struct Heap4 {
+    uint32_t i0, i1, i2, i3;
+    float s0, s1, s2, s3;
+    __device__ void swap01() {
+        uint32_t ti = i0; i0 = i1; i1 = ti;
+        float ts = s0; s0 = s1; s1 = ts;
     }
-}
+    __device__ void swap02() {
+        uint32_t ti = i0; i0 = i2; i2 = ti;
+        float ts = s0; s0 = s2; s2 = ts;
+    }
+    __device__ void swap13() {
+        uint32_t ti = i1; i1 = i3; i3 = ti;
+        float ts = s1; s1 = s3; s3 = ts;
+    }
+    // siftDownMin(start = 1, end): the only child of position 1 is 3.
+    __device__ void sift1(uint32_t end) {
+        if (3 < end && s3 < s1) swap13();
+    }
+    // siftDownMin(start = 0, end).
+    __device__ void sift0(uint32_t end) {
+        uint32_t smallest = 0;
+        float sm = s0;
+        if (1 < end && s1 < sm) {
+            smallest = 1;
+            sm = s1;
+        }
+        if (2 < end && s2 < sm) smallest = 2;
+        if (smallest == 1) {
+            swap01();
+            sift1(end);
+        } else if (smallest == 2) {
+            swap02();  // position 2 has no children below 4
+        }
+    }
+};
 
 // math.topK (math.zig:130-174): heap seeded with the first k scores, later
 // scores replace the root only when strictly greater, results popped from the
-// root into positions k-1, k-2, ... (descending).
-__device__ void top_k(const float* scores, uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK], float (&ts)[kMaxK]) {
-    uint32_t hi[kMaxK];
-    float hs[kMaxK];
-    for (uint32_t i = 0; i < k; ++i) {
-        hi[i] = i;
-        hs[i] = scores[i];
-    }
-    for (uint32_t i = k / 2; i > 0;) {
-        --i;
-        sift_down_min(hi, hs, i, k);
-    }
+// root into positions k-1, k-2, ... (descending). Run by a whole wave for one
+// token: lane l holds scores l, l + 64, l + 128, l + 192 (n <= 256); the scan
+// reads score j with readlane, so the heap's values are uniform registers.
+__device__ float score_at(const float (&sc)[4], uint32_t j) {
+    const float v = j < 64 ? sc[0] : j < 128 ? sc[1] : j < 192 ? sc[2] : sc[3];
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)(j & 63)));
+}
+
+__device__ void top_k_wave(const float (&sc)[4], uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
+                           float (&ts)[kMaxK]) {
+    Heap4 h;
+    h.i0 = 0; h.s0 = score_at(sc, 0);
+    h.i1 = 1; h.s1 = k > 1 ? score_at(sc, 1) : 0.0f;
+    h.i2 = 2; h.s2 = k > 2 ? score_at(sc, 2) : 0.0f;
+    h.i3 = 3; h.s3 = k > 3 ? score_at(sc, 3) : 0.0f;
+    // for (i = k / 2; i > 0;) sift(--i, k)
+    if (k / 2 >= 2) h.sift1(k);
+    if (k / 2 >= 1) h.sift0(k);
     for (uint32_t j = k; j < n; ++j) {
-        const float v = scores[j];
-        if (v > hs[0]) {
-            hi[0] = j;
-            hs[0] = v;
-            sift_down_min(hi, hs, 0, k);
+        const float v = score_at(sc, j);
+        if (v > h.s0) {
+            h.i0 = j;
+            h.s0 = v;
+            h.sift0(k);
         }
     }
-    for (uint32_t ri = k; ri > 0;) {
-        --ri;
-        ids[ri] = hi[0];
-        ts[ri] = hs[0];
-        hi[0] = hi[ri];
-        hs[0] = hs[ri];
-        sift_down_min(hi, hs, 0, ri);
+    // Pop: result[ri] = root; root = heap[ri]; sift(0, ri), ri = k-1 .. 0.
+#pragma unroll
+    for (int ri = kMaxK - 1; ri >= 0; --ri) {
+        if ((uint32_t)ri >= k) continue;
+        ids[ri] = h.i0;
+        ts[ri] = h.s0;
+        if (ri == 3) { h.i0 = h.i3; h.s0 = h.s3; }
+        if (ri == 2) { h.i0 = h.i2; h.s0 = h.s2; }
+        if (ri == 1) { h.i0 = h.i1; h.s0 = h.s1; }
+        h.sift0((uint32_t)ri);
     }
 }
 
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
-    __shared__ uint32_t s_ids[kRouteThreads * kMaxK];
-    __shared__ uint32_t s_act[kRouteThreads];  // bit i: assignment i of the token is computed
-    __shared__ uint32_t s_cnt[kRouteThreads];  // per expert (n_experts <= kRouteThreads)
-    __shared__ uint32_t s_off[kRouteThreads];
-    const uint32_t tid = threadIdx.x;
-    const uint32_t T = a.n_tokens, E = a.n_experts, k = a.k;
+// The common case of topK without the heap: when the k + 1 largest scores
+// are distinct (and no score is NaN), the heap's result is exactly those k in
+// descending order. k + 1 rounds of a wave-wide max find them; a repeated
+// value in any round, or a NaN anywhere, returns false and the caller runs
+// the heap (ties and NaNs make the heap's insertion order matter).
+__device__ bool top_k_distinct(const float (&sc)[4], uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
+                               float (&ts)[kMaxK]) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t valid = 0;
+    bool nan = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (lane + 64 * q < n) {
+            valid |= 1u << q;
+            nan |= sc[q] != sc[q];
+        }
+    if (__any(nan)) return false;
+    const uint32_t rounds = k < n ? k + 1 : k;
+    for (uint32_t r = 0; r < rounds; ++r) {
+        float best = -__builtin_inff();
+        uint32_t best_q = 4, dup = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (!((valid >> q) & 1u)) continue;
+            if (best_q == 4 || sc[q] > best) {
+                best = sc[q];
+                best_q = q;
+                dup = 0;
+            } else if (sc[q] == best) {
+                dup = 1;
+            }
+        }
+        float m = best_q < 4 ? best : -__builtin_inff();
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        const bool mine = best_q < 4 && best == m;
+        const unsigned long long who = __ballot(mine);
+        if (__popcll(who) != 1 || __any(mine && dup)) return false;
+        const uint32_t wl = (uint32_t)__builtin_ctzll(who);
+        const uint32_t wq = (uint32_t)__shfl((int)best_q, (int)wl, 64);
+        if (r < k) {
+            ids[r] = wl + 64 * wq;
+            ts[r] = m;
+        }
+        if (lane == wl) valid &= ~(1u << wq);
+    }
+    return true;
+}
 
-    if (tid < T) {
-        const uint32_t t = tid;
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
+    __shared__ uint32_t s_ids[kMaxTokens * kMaxK];
+    __shared__ uint32_t s_act[kMaxTokens];  // bit i: assignment i of the token is computed
+    __shared__ uint32_t s_cnt[kMaxExperts];   // assignments per expert
+    __shared__ uint32_t s_off[kMaxExperts];   // first slot of each expert
+    __shared__ uint32_t s_choff[kMaxExperts]; // first work item (chunk) of each expert
+    __shared__ uint32_t s_rank[kMaxTokens * kMaxK];
+    __shared__ uint32_t s_nchunks;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63, wave = tid >> 6;
+    const uint32_t T = a.n_tokens, E = a.n_experts, k = a.k;
+    for (uint32_t e = tid; e < E; e += kRouteThreads) s_cnt[e] = 0;
+
+    for (uint32_t t = wave; t < T; t += kRouteThreads / 64) {
+        const BufRsrc sr = make_rsrc(a.scores + (uint64_t)t * E, E * 4);
+        float sc[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sc[q] = __uint_as_float(buf_load_b32(sr, (lane + 64 * q) * 4, 0));
         uint32_t ids[kMaxK] = {0, 0, 0, 0};
         float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f}, w[kMaxK] = {0.f, 0.f, 0.f, 0.f};
-        top_k(a.scores + (uint64_t)t * E, E, k, ids, ts);
+        if (!top_k_distinct(sc, E, k, ids, ts)) top_k_wave(sc, E, k, ids, ts);
         // Softmax over the selected logits, then the routed scaling factor
         // (scheduler.zig:184-201).
         float mx = ts[0];
@@ -98,7 +188,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         }
         for (uint32_t i = 0; i < k; ++i) w[i] = w[i] / sum;
         for (uint32_t i = 0; i < k; ++i) w[i] = w[i] * a.scale;
-        for (uint32_t i = 0; i < k; ++i) atomicAdd(a.counts + ids[i], 1ull);  // stats.record (220-222)
         // Heavy throttle keeps the top expert only and renormalises it
         // (225-242); the others are deferred.
         uint32_t act = (1u << k) - 1u, deferred = 0;
@@ -108,20 +197,21 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
             const float rem = 0.0f + w[0];
             if (rem > 0.0f) w[0] = w[0] * (a.scale / rem);
         }
-        // RouteResult as moeFFN sees it (after the fallback).
-        if (a.route_ids)
-            for (uint32_t i = 0; i < kMaxK; ++i) a.route_ids[t * kMaxK + i] = i < k ? ids[i] : 0xFFFFFFFFu;
-        if (a.route_w)
-            for (uint32_t i = 0; i < kMaxK; ++i) a.route_w[t * kMaxK + i] = i < k ? w[i] : 0.0f;
-        for (uint32_t i = 0; i < kMaxK; ++i) {
-            s_ids[t * kMaxK + i] = ids[i];
-            a.assign_w[t * kMaxK + i] = ((act >> i) & 1u) ? w[i] : 0.0f;
-            a.assign_slot[t * kMaxK + i] = -1;
+        if (lane == 0) {
+            for (uint32_t i = 0; i < k; ++i) atomicAdd(a.counts + ids[i], 1ull);  // stats.record (220-222)
+            // RouteResult as moeFFN sees it (after the fallback).
+            for (uint32_t i = 0; i < kMaxK; ++i) {
+                if (a.route_ids) a.route_ids[t * kMaxK + i] = i < k ? ids[i] : 0xFFFFFFFFu;
+                if (a.route_w) a.route_w[t * kMaxK + i] = i < k ? w[i] : 0.0f;
+                s_ids[t * kMaxK + i] = ids[i];
+                a.assign_w[t * kMaxK + i] = ((act >> i) & 1u) ? w[i] : 0.0f;
+                a.assign_slot[t * kMaxK + i] = -1;
+            }
+            s_act[t] = act;
+            a.deferred[t] = deferred;
+            a.shared_slot[t] = a.shared ? (int32_t)(4 * T + t) : -1;
+            a.slot_tok[4 * T + t] = t;
         }
-        s_act[t] = act;
-        a.deferred[t] = deferred;
-        a.shared_slot[t] = a.shared ? (int32_t)(4 * T + t) : -1;
-        a.slot_tok[4 * T + t] = t;
     }
     __syncthreads();
 
@@ -151,53 +241,72 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         return;
     }
 
-    // Prefill: assignments sorted by expert, tokens in order within an expert.
-    for (uint32_t e = tid; e < E; e += kRouteThreads) {
-        uint32_t c = 0;
-        for (uint32_t t = 0; t < T; ++t)
-            for (uint32_t i = 0; i < k; ++i) c += (((s_act[t] >> i) & 1u) && s_ids[t * kMaxK + i] == e) ? 1u : 0u;
-        s_cnt[e] = c;
+    // Prefill: assignments grouped by expert. An assignment's rank inside its
+    // expert group comes from an LDS counter; rows of a group are independent,
+    // so the order inside a group does not change any result.
+    for (uint32_t p = tid; p < T * kMaxK; p += kRouteThreads) {
+        const uint32_t t = p / kMaxK, i = p % kMaxK;
+        if (i < k && ((s_act[t] >> i) & 1u)) s_rank[p] = atomicAdd(&s_cnt[s_ids[p]], 1u);
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t off = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            s_off[e] = off;
-            off += s_cnt[e];
-        }
-    }
-    __syncthreads();
-    for (uint32_t e = tid; e < E; e += kRouteThreads) {
-        uint32_t r = s_off[e];
-        for (uint32_t t = 0; t < T; ++t)
-            for (uint32_t i = 0; i < k; ++i)
-                if (((s_act[t] >> i) & 1u) && s_ids[t * kMaxK + i] == e) {
-                    a.assign_slot[t * kMaxK + i] = (int32_t)r;
-                    a.slot_tok[r] = t;
-                    ++r;
+    if (wave == 0) {
+        // Exclusive scans over experts: slot offsets and chunk (work item) offsets.
+        uint32_t carry = 0, carry_ch = 0;
+        for (uint32_t base = 0; base < E; base += 64) {
+            const uint32_t e = base + lane;
+            const uint32_t c = e < E ? s_cnt[e] : 0u;
+            const uint32_t ch = (c + kQmmTokens - 1) / kQmmTokens;
+            uint32_t inc = c, inc_ch = ch;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t u = (uint32_t)__shfl_up((int)inc, off, 64);
+                const uint32_t uch = (uint32_t)__shfl_up((int)inc_ch, off, 64);
+                if (lane >= (uint32_t)off) {
+                    inc += u;
+                    inc_ch += uch;
                 }
+            }
+            if (e < E) {
+                s_off[e] = carry + inc - c;
+                s_choff[e] = carry_ch + inc_ch - ch;
+            }
+            carry += (uint32_t)__shfl((int)inc, 63, 64);
+            carry_ch += (uint32_t)__shfl((int)inc_ch, 63, 64);
+        }
+        if (lane == 0) s_nchunks = carry_ch;
+    }
+    __syncthreads();
+    for (uint32_t p = tid; p < T * kMaxK; p += kRouteThreads) {
+        const uint32_t t = p / kMaxK, i = p % kMaxK;
+        if (i < k && ((s_act[t] >> i) & 1u)) {
+            const uint32_t slot = s_off[s_ids[p]] + s_rank[p];
+            a.assign_slot[p] = (int32_t)slot;
+            a.slot_tok[slot] = t;
+        }
+    }
+    // Work items: chunk c of expert e is item s_choff[e] + c (gate and up
+    // interleaved in the gate/up list); the shared expert's chunks follow.
+    for (uint32_t e = tid; e < E; e += kRouteThreads) {
+        const uint32_t c = s_cnt[e], off = s_off[e], ch0 = s_choff[e];
+        for (uint32_t c0 = 0, q = ch0; c0 < c; c0 += kQmmTokens, ++q) {
+            const uint32_t m = min(kQmmTokens, c - c0);
+            a.work_gu[2 * q] = QmmWork{e, off + c0, m, 0};
+            a.work_gu[2 * q + 1] = QmmWork{E + e, off + c0, m, a.inter};
+            a.work_dn[q] = QmmWork{e, off + c0, m, 0};
+        }
+    }
+    const uint32_t nch = s_nchunks;
+    const bool sh = a.shared && a.shared_merged;
+    const uint32_t sh_chunks = sh ? (T + kQmmTokens - 1) / kQmmTokens : 0;
+    for (uint32_t c = tid; c < sh_chunks; c += kRouteThreads) {
+        const uint32_t c0 = c * kQmmTokens, m = min(kQmmTokens, T - c0), q = nch + c;
+        a.work_gu[2 * q] = QmmWork{2 * E, 4 * T + c0, m, 0};
+        a.work_gu[2 * q + 1] = QmmWork{2 * E + 1, 4 * T + c0, m, a.inter};
+        a.work_dn[q] = QmmWork{E, 4 * T + c0, m, 0};
     }
     if (tid == 0) {
-        uint32_t ng = 0, nd = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            const uint32_t c = s_cnt[e], off = s_off[e];
-            for (uint32_t c0 = 0; c0 < c; c0 += kQmmTokens) {
-                const uint32_t m = min(kQmmTokens, c - c0);
-                a.work_gu[ng++] = QmmWork{e, off + c0, m, 0};
-                a.work_gu[ng++] = QmmWork{E + e, off + c0, m, a.inter};
-                a.work_dn[nd++] = QmmWork{e, off + c0, m, 0};
-            }
-        }
-        if (a.shared && a.shared_merged) {
-            for (uint32_t c0 = 0; c0 < T; c0 += kQmmTokens) {
-                const uint32_t m = min(kQmmTokens, T - c0);
-                a.work_gu[ng++] = QmmWork{2 * E, 4 * T + c0, m, 0};
-                a.work_gu[ng++] = QmmWork{2 * E + 1, 4 * T + c0, m, a.inter};
-                a.work_dn[nd++] = QmmWork{E, 4 * T + c0, m, 0};
-            }
-        }
-        a.n_work[0] = ng;
-        a.n_work[1] = nd;
+        a.n_work[0] = 2 * (nch + sh_chunks);
+        a.n_work[1] = nch + sh_chunks;
     }
 }
 
@@ -230,7 +339,7 @@ uint32_t route_max_work(uint32_t n_tokens, uint32_t n_experts) {
 }
 
 hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
-    if (a.n_tokens == 0 || a.n_tokens > kRouteThreads || a.n_experts > kRouteThreads || a.k == 0 || a.k > kMaxK ||
+    if (a.n_tokens == 0 || a.n_tokens > kMaxTokens || a.n_experts > kMaxExperts || a.k == 0 || a.k > kMaxK ||
         a.k > a.n_experts)
         return hipErrorInvalidValue;
     route_kernel<<<1, kRouteThreads, 0, s>>>(a);

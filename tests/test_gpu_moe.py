@@ -244,3 +244,31 @@ def test_invalid_calls(ctx, orc):
             gpu.ffn(np.zeros((257, SMALL["H"]), np.float32))
     finally:
         gpu.free()
+
+
+@pytest.mark.parametrize("level", [0, 1, 2, 3])
+def test_routing_ties_follow_the_heap(ctx, orc, level):
+    """Exact score ties: under an identity router the scores are the hidden
+    states' first E coordinates, bit-identical on both sides, drawn from four
+    values so that most tokens tie at the k-th place. The selected ids and
+    their order must be the min-heap's (math.zig:130-174), not a sort's."""
+    rng = np.random.default_rng(400 + level)
+    H, I, E, T = 512, 256, 64, 64
+    _, gate, up, down, shared = _weights(rng, mm.IQ2_XXS, H, I, E, shared_inter=I)
+    router = np.zeros((E, H), dtype=np.float32)
+    router[:, :E] = np.eye(E, dtype=np.float32)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    h[:, :E] = rng.choice(np.array([-1.0, 0.0, 0.5, 1.0], dtype=np.float32), (T, E))
+    gpu, cpu = _layers(ctx, orc, mm.IQ2_XXS, H, I, E, router, gate, up, down, shared, shared_inter=I)
+    try:
+        out_g, ids_g, w_g = gpu.ffn(h, level=level)
+        out_c, ids_c, w_c = cpu.ffn(h, level=level)
+        np.testing.assert_array_equal(ids_g, ids_c)
+        np.testing.assert_allclose(w_g, w_c, rtol=TOL_W, atol=1e-7)
+        assert mm.max_abs_rel(out_g, out_c) < TOL_OUT
+        # the ties are real: the k-th and (k+1)-th scores are equal for most tokens
+        k = ids_c.shape[1]
+        srt = -np.sort(-h[:, :E], axis=1)
+        assert (srt[:, k - 1] == srt[:, k]).mean() > 0.5
+    finally:
+        gpu.free()
