@@ -367,6 +367,57 @@ class MoeLayer:
 
 
 # ----------------------------------------------------------------------------
+# Operator planner (OpScheduler / LayerPlan, scheduler.zig:265-552); host only
+# ----------------------------------------------------------------------------
+
+OP = dict(matMulQ8_0=0, matMulQ4_K=1, matMulF32=2, matVecMulQ8_0=3, matVecMulF32=4, rmsNorm=5, siluMul=6, rope=7,
+          softmax=8, dot=9, attention=10, ffn_gate_up=11, ffn_down=12)
+PREC = dict(q8_0=0, q4_k=1, f32=2, f16=3, iq2_xxs=4)
+BACKEND_CPU, BACKEND_GPU, BACKEND_NPU = 0, 1, 2
+
+
+def plan_layer(layer: int, *, hidden_size: int, intermediate_size: int, num_heads: int, head_dim: int,
+               leading_dense_layers: int, n_routed_experts: int, weight_precision: int = 0, seq_len_hint: int = 0,
+               has_gpu: bool = False, has_npu: bool = False, throttle_level: int = 0, perf_db=()):
+    """OpScheduler.init + planLayer. perf_db: iterable of (op, precision,
+    (m, n, k, dim), cpu_us, gpu_us). Returns a list of OpSchedule."""
+    lib = load_library()
+    hp = PlanHParams(hidden_size, intermediate_size, num_heads, head_dim, seq_len_hint, leading_dense_layers,
+                     n_routed_experts, weight_precision)
+    entries = (PerfEntry * max(1, len(perf_db)))()
+    for i, (op, prec, shp, cpu_us, gpu_us) in enumerate(perf_db):
+        entries[i].op, entries[i].precision = op, prec
+        entries[i].shape = Shape(*shp)
+        entries[i].cpu_us, entries[i].gpu_us = cpu_us, gpu_us
+    out = (OpSchedule * 16)()
+    n = ctypes.c_size_t()
+    check(lib.mmhip_plan_layer(layer, ctypes.byref(hp), int(has_gpu), int(has_npu), throttle_level, entries,
+                               len(perf_db), out, 16, ctypes.byref(n)), "mmhip_plan_layer")
+    return list(out[:n.value])
+
+
+def _ops_array(ops):
+    arr = (OpSchedule * max(1, len(ops)))()
+    for i, o in enumerate(ops):
+        arr[i] = o
+    return arr
+
+
+def plan_critical_path_us(ops) -> int:
+    """LayerPlan.estimatedCriticalPathUs."""
+    return load_library().mmhip_plan_critical_path_us(_ops_array(ops), len(ops))
+
+
+def plan_device_mask(ops) -> int:
+    """LayerPlan.deviceMask (bit 0 CPU, 1 GPU, 2 NPU)."""
+    return load_library().mmhip_plan_device_mask(_ops_array(ops), len(ops))
+
+
+def op_schedule(op: int, backend: int, precision: int, estimated_us: int, sync_after: bool, shape=(0, 0, 0, 0)):
+    return OpSchedule(op, backend, precision, int(sync_after), Shape(*shape), estimated_us)
+
+
+# ----------------------------------------------------------------------------
 # Seeded synthetic weights (raw GGUF bytes)
 # ----------------------------------------------------------------------------
 

@@ -1,0 +1,257 @@
+// HIP backend for the quantized-weight matrix path (MI355X / gfx950).
+//
+// Zig side of libmmhip (include/mmhip.h). It takes the place the OpenCL and
+// Metal backends hold in the engine: same object shape as OpenCLBackend
+// (isAvailable / init / deinit / op methods on host slices,
+// src/opencl_backend.zig:55-537), same C-bridge conventions as
+// metal_backend.zig (extern fn, status codes mapped to Zig errors,
+// src/metal_backend.zig:7-46). Place this file next to inference.zig and link
+// with linkSystemLibrary("mmhip") and linkSystemLibrary("amdhip64").
+//
+// Every compute method returns an error when the device is unusable; the
+// caller keeps the reference's CPU fallback (src/inference.zig:1209-1213).
+
+const std = @import("std");
+const gguf = @import("gguf.zig");
+
+// ---- C ABI (include/mmhip.h) ----
+
+pub const Ctx = opaque {};
+pub const Weight = opaque {};
+pub const MoeLayerHandle = opaque {};
+
+pub const MoeWeights = extern struct {
+    hidden_size: u32,
+    moe_intermediate: u32,
+    shared_intermediate: u32,
+    n_routed_experts: u32,
+    expert_type: u32,
+    shared_type: u32,
+    router_type: u32,
+    routed_scaling_factor: f32,
+    router_host: ?*const anyopaque,
+    expert_gate_host: ?*const anyopaque,
+    expert_up_host: ?*const anyopaque,
+    expert_down_host: ?*const anyopaque,
+    shared_gate_host: ?*const anyopaque = null,
+    shared_up_host: ?*const anyopaque = null,
+    shared_down_host: ?*const anyopaque = null,
+};
+
+pub const RouteParams = extern struct {
+    throttle_level: i32 = 0,
+    active_expert_limit: u32 = 0,
+    deferral_bias_host: ?[*]const f32 = null,
+};
+
+pub const Shape = extern struct { m: u32 = 0, n: u32 = 0, k: u32 = 0, dim: u32 = 0 };
+
+pub const OpSchedule = extern struct {
+    op: u32,
+    backend: u32,
+    precision: u32,
+    sync_after: u32,
+    shape: Shape,
+    estimated_us: u64,
+};
+
+pub const PlanHyperParams = extern struct {
+    hidden_size: u32,
+    intermediate_size: u32,
+    num_heads: u32,
+    head_dim: u32,
+    seq_len_hint: u32 = 0,
+    leading_dense_layers: u32,
+    n_routed_experts: u32,
+    weight_precision: u32,
+};
+
+pub const PerfEntry = extern struct {
+    op: u32,
+    precision: u32,
+    shape: Shape,
+    cpu_us: u64,
+    gpu_us: u64,
+};
+
+pub const max_moe_tokens: u32 = 256;
+
+extern fn mmhip_last_error() [*:0]const u8;
+extern fn mmhip_is_available() c_int;
+extern fn mmhip_device_count() c_int;
+extern fn mmhip_version() [*:0]const u8;
+extern fn mmhip_init(out_ctx: *?*Ctx, device: c_int) c_int;
+extern fn mmhip_destroy(ctx: ?*Ctx) void;
+extern fn mmhip_synchronize(ctx: *Ctx) c_int;
+extern fn mmhip_stream(ctx: *Ctx) ?*anyopaque;
+extern fn mmhip_num_cu(ctx: *Ctx) c_int;
+extern fn mmhip_profile_enable(ctx: *Ctx, enable: c_int) c_int;
+extern fn mmhip_profile_read(ctx: *Ctx, family: [*:0]const u8, total_ms: *f64, launches: *u64) c_int;
+extern fn mmhip_malloc(ctx: *Ctx, out_dev: *?*anyopaque, bytes: usize) c_int;
+extern fn mmhip_free(ctx: *Ctx, dev: ?*anyopaque) c_int;
+extern fn mmhip_memcpy_h2d(ctx: *Ctx, dst_dev: ?*anyopaque, src_host: ?*const anyopaque, bytes: usize) c_int;
+extern fn mmhip_memcpy_d2h(ctx: *Ctx, dst_host: ?*anyopaque, src_dev: ?*const anyopaque, bytes: usize) c_int;
+extern fn mmhip_memset_dev(ctx: *Ctx, dst_dev: ?*anyopaque, value: c_int, bytes: usize) c_int;
+extern fn mmhip_weight_upload(ctx: *Ctx, raw_host: ?*const anyopaque, type_: u32, rows: u64, cols: u64, count: u64, out_w: *?*Weight) c_int;
+extern fn mmhip_weight_from_device(ctx: *Ctx, raw_dev: ?*const anyopaque, type_: u32, rows: u64, cols: u64, count: u64, out_w: *?*Weight) c_int;
+extern fn mmhip_weight_free(ctx: *Ctx, w: ?*Weight) void;
+extern fn mmhip_weight_device_bytes(w: *const Weight) u64;
+extern fn mmhip_mat_vec_mul(ctx: *Ctx, out_host: [*]f32, ptr_host: ?*const anyopaque, type_: u32, x_host: [*]const f32, out_dim: u64, in_dim: u64) c_int;
+extern fn mmhip_batch_mat_mul(ctx: *Ctx, out_host: [*]f32, ptr_host: ?*const anyopaque, type_: u32, in_host: [*]const f32, out_dim: u64, batch: u64, in_dim: u64) c_int;
+extern fn mmhip_dequantize(ctx: *Ctx, out_host: [*]f32, data_host: ?*const anyopaque, type_: u32, n_elements: u64) c_int;
+extern fn mmhip_forget(ctx: *Ctx, ptr_host: ?*const anyopaque) c_int;
+extern fn mmhip_dequantize_dev(ctx: *Ctx, out_dev: ?*anyopaque, raw_dev: ?*const anyopaque, type_: u32, n_elements: u64) c_int;
+extern fn mmhip_gemv_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque) c_int;
+extern fn mmhip_gemv_batched_dev(ctx: *Ctx, w: *const Weight, first: u64, n_mats: u64, x_dev: ?*const anyopaque, x_stride: u64, y_dev: ?*anyopaque, y_stride: u64) c_int;
+extern fn mmhip_qmm_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque, batch: u64, out_layout: c_int) c_int;
+extern fn mmhip_moe_layer_create(ctx: *Ctx, wts: *const MoeWeights, out_layer: *?*MoeLayerHandle) c_int;
+extern fn mmhip_moe_layer_destroy(ctx: *Ctx, layer: ?*MoeLayerHandle) void;
+extern fn mmhip_moe_ffn(ctx: *Ctx, layer: *MoeLayerHandle, hidden_host: [*]const f32, out_host: [*]f32, n_tokens: u32, rp: ?*const RouteParams, route_ids_host: ?[*]u32, route_weights_host: ?[*]f32) c_int;
+extern fn mmhip_moe_ffn_dev(ctx: *Ctx, layer: *MoeLayerHandle, hidden_dev: ?*const anyopaque, out_dev: ?*anyopaque, n_tokens: u32, rp: ?*const RouteParams, route_ids_dev: ?*anyopaque, route_weights_dev: ?*anyopaque) c_int;
+extern fn mmhip_moe_expert_counts(ctx: *Ctx, layer: *MoeLayerHandle, counts_host: [*]u64) c_int;
+extern fn mmhip_plan_layer(layer: u32, hp: *const PlanHyperParams, has_gpu: c_int, has_npu: c_int, throttle_level: c_int, db: ?[*]const PerfEntry, db_len: usize, out: [*]OpSchedule, cap: usize, n_out: *usize) c_int;
+extern fn mmhip_plan_critical_path_us(ops: [*]const OpSchedule, n: usize) u64;
+extern fn mmhip_plan_device_mask(ops: [*]const OpSchedule, n: usize) u32;
+
+// ---- errors ----
+
+pub const HipError = error{
+    HipUnavailable,
+    HipInvalidArgument,
+    HipUnsupportedType,
+    HipLaunch,
+    HipOutOfMemory,
+};
+
+fn check(rc: c_int) HipError!void {
+    if (rc >= 0) return;
+    std.log.debug("libmmhip: {s}", .{mmhip_last_error()});
+    return switch (rc) {
+        -1 => error.HipUnavailable,
+        -2 => error.HipInvalidArgument,
+        -3 => error.HipUnsupportedType,
+        -5 => error.HipOutOfMemory,
+        else => error.HipLaunch,
+    };
+}
+
+/// A gfx950 device is present and the library loaded (OpenCLBackend.isAvailable).
+pub fn isAvailable() bool {
+    return mmhip_is_available() == 1;
+}
+
+pub fn lastError() [*:0]const u8 {
+    return mmhip_last_error();
+}
+
+// ---- backend object ----
+
+pub const HipBackend = struct {
+    ctx: *Ctx,
+    allocator: std.mem.Allocator,
+
+    const Self = @This();
+
+    /// OpenCLBackend.init: one context on device 0.
+    pub fn init(allocator: std.mem.Allocator) !Self {
+        var ctx: ?*Ctx = null;
+        try check(mmhip_init(&ctx, 0));
+        return .{ .ctx = ctx.?, .allocator = allocator };
+    }
+
+    /// OpenCLBackend.deinit: frees the resident weights and the context.
+    pub fn deinit(self: *Self) void {
+        mmhip_destroy(self.ctx);
+    }
+
+    /// matVecMulUnified (inference.zig:1200-1228) on the device: out = W . x
+    /// for Q8_0 / IQ2_XXS / F32 / F16 weights given as mmap'd GGUF bytes.
+    /// The weight is uploaded on first use and stays resident, keyed by its
+    /// host address (getOrUploadMatBuffer's role).
+    pub fn matVecMulUnified(self: *Self, out: []f32, ptr: [*]const u8, type_: gguf.GgmlType, x: []const f32, out_dim: usize, in_dim: usize) !void {
+        std.debug.assert(out.len >= out_dim and x.len >= in_dim);
+        try check(mmhip_mat_vec_mul(self.ctx, out.ptr, ptr, @intFromEnum(type_), x.ptr, out_dim, in_dim));
+    }
+
+    /// batchMatMulUnified (1231-1264): out [batch][out_dim].
+    pub fn batchMatMulUnified(self: *Self, out: []f32, ptr: [*]const u8, type_: gguf.GgmlType, in: []const f32, out_dim: usize, batch: usize, in_dim: usize) !void {
+        std.debug.assert(out.len >= out_dim * batch and in.len >= in_dim * batch);
+        try check(mmhip_batch_mat_mul(self.ctx, out.ptr, ptr, @intFromEnum(type_), in.ptr, out_dim, batch, in_dim));
+    }
+
+    /// OpenCLBackend.matMulQ8_0 (opencl_backend.zig:412-453): a Q8_0 GEMV
+    /// despite the name.
+    pub fn matMulQ8_0(self: *Self, out: []f32, mat: []const u8, vec: []const f32, out_dim: u32, in_dim: u32) !void {
+        try self.matVecMulUnified(out, mat.ptr, .q8_0, vec, out_dim, in_dim);
+    }
+
+    /// dequant.dequantize (dequant.zig:632-659) on the device, bit-exact.
+    pub fn dequantize(self: *Self, out: []f32, data: [*]const u8, type_: gguf.GgmlType) !void {
+        try check(mmhip_dequantize(self.ctx, out.ptr, data, @intFromEnum(type_), out.len));
+    }
+
+    /// Drops the resident copy of a weight (e.g. before unmapping the file).
+    pub fn forget(self: *Self, ptr: [*]const u8) void {
+        _ = mmhip_forget(self.ctx, ptr);
+    }
+
+    pub fn synchronize(self: *Self) !void {
+        try check(mmhip_synchronize(self.ctx));
+    }
+};
+
+// ---- MoE FFN layer (moeFFN + Scheduler.route on the device) ----
+
+pub const MoeLayer = struct {
+    backend: *HipBackend,
+    handle: *MoeLayerHandle,
+    hidden: u32,
+
+    /// Uploads one layer's router, routed experts and shared expert.
+    pub fn create(backend: *HipBackend, w: MoeWeights) !MoeLayer {
+        var h: ?*MoeLayerHandle = null;
+        try check(mmhip_moe_layer_create(backend.ctx, &w, &h));
+        return .{ .backend = backend, .handle = h.?, .hidden = w.hidden_size };
+    }
+
+    pub fn destroy(self: *MoeLayer) void {
+        mmhip_moe_layer_destroy(self.backend.ctx, self.handle);
+    }
+
+    /// moeFFN for n tokens (hidden / out: [n][hidden]); route ids and weights
+    /// ([n][4]) as Scheduler.route returns them. Returns k.
+    pub fn ffn(self: *MoeLayer, hidden: []const f32, out: []f32, n_tokens: u32, rp: RouteParams, route_ids: ?[]u32, route_weights: ?[]f32) !u32 {
+        std.debug.assert(n_tokens >= 1 and n_tokens <= max_moe_tokens);
+        std.debug.assert(hidden.len >= n_tokens * self.hidden and out.len >= n_tokens * self.hidden);
+        const rc = mmhip_moe_ffn(self.backend.ctx, self.handle, hidden.ptr, out.ptr, n_tokens, &rp, if (route_ids) |r| r.ptr else null, if (route_weights) |r| r.ptr else null);
+        try check(rc);
+        return @intCast(rc);
+    }
+
+    /// ExpertStats.counts of this layer.
+    pub fn expertCounts(self: *MoeLayer, counts: []u64) !void {
+        try check(mmhip_moe_expert_counts(self.backend.ctx, self.handle, counts.ptr));
+    }
+};
+
+// ---- operator planner (OpScheduler.planLayer with the GPU rules) ----
+
+/// Plans one layer (RMSNorm, attention, RMSNorm, FFN); `out` receives the
+/// ops. Returns the number written.
+pub fn planLayer(layer: u32, hp: PlanHyperParams, has_gpu: bool, has_npu: bool, throttle_level: i32, db: []const PerfEntry, out: []OpSchedule) !usize {
+    var n: usize = 0;
+    try check(mmhip_plan_layer(layer, &hp, @intFromBool(has_gpu), @intFromBool(has_npu), throttle_level, if (db.len > 0) db.ptr else null, db.len, out.ptr, out.len, &n));
+    return n;
+}
+
+pub fn criticalPathUs(ops: []const OpSchedule) u64 {
+    return mmhip_plan_critical_path_us(ops.ptr, ops.len);
+}
+
+pub fn deviceMask(ops: []const OpSchedule) u8 {
+    return @intCast(mmhip_plan_device_mask(ops.ptr, ops.len));
+}
+
+test "HipBackend reports availability without crashing" {
+    _ = isAvailable();
+}
