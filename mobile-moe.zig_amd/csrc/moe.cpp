@@ -410,7 +410,8 @@ int mmhip_moe_ffn_dev(mmhip_ctx* ctx, mmhip_moe_layer* layer, const float* hidde
     uint32_t k;
     int rc = call_params(layer, n_tokens, rp, &level, &k);
     if (rc != MMHIP_OK) return rc;
-    std::lock_guard<std::mutex> lock(layer->mu);
+    std::lock_guard<std::mutex> lock(layer->mu);  // then the context: no caller takes them in the other order
+    std::lock_guard<std::mutex> ctx_lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
     bool with_bias;
     rc = upload_bias(ctx, layer, rp, &with_bias);
@@ -430,7 +431,8 @@ int mmhip_moe_ffn(mmhip_ctx* ctx, mmhip_moe_layer* layer, const float* hidden_ho
     uint32_t k;
     int rc = call_params(layer, n_tokens, rp, &level, &k);
     if (rc != MMHIP_OK) return rc;
-    std::lock_guard<std::mutex> lock(layer->mu);
+    std::lock_guard<std::mutex> lock(layer->mu);  // then the context: no caller takes them in the other order
+    std::lock_guard<std::mutex> ctx_lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
     const size_t bytes = (size_t)n_tokens * layer->hidden * 4;
     hipStream_t s = ctx->stream;
@@ -460,7 +462,8 @@ int mmhip_moe_expert_counts(mmhip_ctx* ctx, mmhip_moe_layer* layer, uint64_t* co
         set_error(MMHIP_ERR_INVALID, "moe_expert_counts: null argument");
         return MMHIP_ERR_INVALID;
     }
-    std::lock_guard<std::mutex> lock(layer->mu);
+    std::lock_guard<std::mutex> lock(layer->mu);  // then the context: no caller takes them in the other order
+    std::lock_guard<std::mutex> ctx_lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipMemcpyAsync(counts_host, layer->counts, (size_t)layer->n_experts * 8, hipMemcpyDeviceToHost,
                                   ctx->stream);
