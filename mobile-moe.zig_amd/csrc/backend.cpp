@@ -312,7 +312,8 @@ int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float*
     const uint64_t ld = out_layout == 0 ? w->rows : batch;
     {
         TimedLaunch tl(ctx, "qmm");
-        e = launch_qmm(w->recs, w->dvals, g, mat, q, (uint32_t)batch, y, ld, out_layout, ctx->stream);
+        e = launch_group_dense(w->recs, w->dvals, g, mat, q, (uint32_t)batch, y, ld, out_layout, ctx->num_cu,
+                               ctx->stream);
     }
     return e == hipSuccess ? MMHIP_OK : hip_fail(e, "qmm: launch");
 }

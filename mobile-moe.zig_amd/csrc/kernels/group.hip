@@ -1,0 +1,380 @@
+// Quantised matmul over groups of 8 activation rows on gfx950: prompt prefill
+// (qmm.matMulQ8_0's role, qmm.zig:58-138) and the MoE experts of a batch
+// grouped by expert (moeFFN over forwardBatch's tokens, inference.zig:346-351,
+// 886-1188).
+//
+// An item is one weight matrix and up to 8 activation rows: consecutive rows
+// of a batch (dense) or the slots of one expert (grouped, items written by the
+// route kernel). The activations arrive quantised (two int8 digit planes +
+// per-block scales) and are staged into LDS so that row j's digits are the A
+// rows 2j / 2j+1 of v_mfma_i32_16x16x32_i8: all 16 A rows carry data, and each
+// weight unit's B operands (IQ2_XXS table lookups or raw Q8_0 bytes) are built
+// once for 8 rows. Lane (n, g) ends with rows 2g and 2g+1 of weight row n; no
+// cross-lane reduction is needed.
+//
+// Streaming is the decode GEMV's: unconditional buffer loads, a ring of three
+// register buffers, an LDS-only barrier, tables built from the grid.
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "tile_ops.hpp"
+
+#include <cstdlib>
+#include <map>
+#include <mutex>
+
+namespace mmhip {
+
+namespace {
+
+constexpr uint32_t kGRows = 8;            // activation rows per item
+constexpr uint32_t kGChunkBlocks = 64;    // 2048 columns of activations per LDS chunk
+constexpr uint32_t kGStage = kGChunkBlocks / 2 * 64;  // 16-byte A chunks per LDS chunk
+
+struct GroupArgs {
+    const uint4* recs;
+    const uint16_t* dvals;
+    uint64_t rec_stride, d_stride;
+    uint32_t d_row;
+    const int8_t* xh;
+    const int8_t* xl;
+    const float* xs;
+    uint64_t xq_stride, xs_stride;
+    const uint32_t* a_row;          // slot -> activation row (grouped), or null
+    float* y;
+    uint64_t y_slot, y_row;         // y[slot * y_slot + col_off + row * y_row]
+    const QmmWork* work;            // grouped when non-null
+    const uint32_t* n_work;
+    uint64_t mat;                   // dense: matrix
+    uint32_t batch;                 // dense: rows of the batch
+    uint32_t tiles, units, rows;
+    uint32_t tiles_per_wg;
+};
+
+// LDS A layout of one chunk: block pair p (blocks 2p, 2p+1) is 1 KiB; lane
+// (n, g)'s 16 bytes at p * 1024 + lane * 16 hold A row n (activation row n/2,
+// digit n&1), columns 8g..8g+7 of block 2p, then of block 2p+1. Lanes read
+// consecutive 16-byte words: no bank conflicts.
+__device__ __forceinline__ void lds_a_pair(const uint8_t* aq, uint32_t pair, uint32_t lane, long& a0, long& a1) {
+    const uint4 q = *reinterpret_cast<const uint4*>(aq + pair * 1024 + lane * 16);
+    a0 = (long)(((uint64_t)q.y << 32) | q.x);
+    a1 = (long)(((uint64_t)q.w << 32) | q.z);
+}
+
+// One step of UPS IQ2_XXS units (unit u = 256 columns = 4 block pairs) for 8
+// activation rows; xs_lds[j * nb + b] = scale of row j, block b of the chunk.
+template <int UPS>
+__device__ __forceinline__ void step_group_iq2(const uint4 (&r)[kMaxUnitsPerStep], const uint32_t (&dw)[kMaxUnitsPerStep],
+                                               uint32_t ub, const uint8_t* aq, const float* xs0, const float* xs1,
+                                               const uint32_t* tab, uint32_t lane, float& acc0, float& acc1) {
+    const uint32_t g = lane >> 4;
+    long b[2][8];
+    iq2_decode_unit(r[0], tab, b[0]);
+#pragma unroll
+    for (int i = 0; i < UPS; ++i) {
+        const int cur = i & 1, nxt = cur ^ 1;
+        long av[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lds_a_pair(aq, (ub + i) * 4 + q, lane, av[2 * q], av[2 * q + 1]);
+        const uint32_t blk0 = (ub + i) * 8;
+        const float4 x0a = *reinterpret_cast<const float4*>(xs0 + blk0);
+        const float4 x0b = *reinterpret_cast<const float4*>(xs0 + blk0 + 4);
+        const float4 x1a = *reinterpret_cast<const float4*>(xs1 + blk0);
+        const float4 x1b = *reinterpret_cast<const float4*>(xs1 + blk0 + 4);
+        const float x0[8] = {x0a.x, x0a.y, x0a.z, x0a.w, x0b.x, x0b.y, x0b.z, x0b.w};
+        const float x1[8] = {x1a.x, x1a.y, x1a.z, x1a.w, x1b.x, x1b.y, x1b.z, x1b.w};
+        const uint32_t ls = iq2_ls_all(r[i], g);
+        if (i + 1 < UPS) iq2_decode_unit(r[i + 1], tab, b[nxt]);
+        const float dq = f16_scale(iq2_scale_bits<UPS>(dw, i)) * 0.25f;
+        const float hdq = dq * 0.5f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const v4i dv = mfma_i8(av[s], b[cur][s]);
+            const float ws = fmaf((float)((ls >> (4 * s)) & 15u), dq, hdq);
+            acc0 = fmaf((float)digits_combine(dv[0], dv[1]), ws * x0[s], acc0);
+            acc1 = fmaf((float)digits_combine(dv[2], dv[3]), ws * x1[s], acc1);
+        }
+    }
+}
+
+// Q8_0: unit u = 64 columns = block pair u.
+template <int UPS>
+__device__ __forceinline__ void step_group_q8(const uint4 (&r)[kMaxUnitsPerStep], const uint32_t (&dw)[kMaxUnitsPerStep],
+                                              uint32_t ub, const uint8_t* aq, const float* xs0, const float* xs1,
+                                              uint32_t lane, float& acc0, float& acc1) {
+#pragma unroll
+    for (int i = 0; i < UPS; ++i) {
+        long a0, a1;
+        lds_a_pair(aq, ub + i, lane, a0, a1);
+        const uint32_t blk0 = (ub + i) * 2;
+        const float2 x0 = *reinterpret_cast<const float2*>(xs0 + blk0);
+        const float2 x1 = *reinterpret_cast<const float2*>(xs1 + blk0);
+        const uint4& rr = r[i];
+        const v4i d0 = mfma_i8(a0, (long)(((uint64_t)rr.y << 32) | rr.x));
+        const v4i d1 = mfma_i8(a1, (long)(((uint64_t)rr.w << 32) | rr.z));
+        const float w0 = f16_scale(dw[i] & 0xFFFFu), w1 = f16_scale(dw[i] >> 16);
+        acc0 = fmaf((float)digits_combine(d0[0], d0[1]), w0 * x0.x, acc0);
+        acc1 = fmaf((float)digits_combine(d0[2], d0[3]), w0 * x1.x, acc1);
+        acc0 = fmaf((float)digits_combine(d1[0], d1[1]), w1 * x0.y, acc0);
+        acc1 = fmaf((float)digits_combine(d1[2], d1[3]), w1 * x1.y, acc1);
+    }
+}
+
+template <int FMT, int UPS, int WG>
+__global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArgs a) {
+    constexpr uint32_t kWaves = WG / 64;
+    constexpr uint32_t kBlkPerUnit = (FMT == kFmtIq2) ? 8 : 2;
+    __shared__ __align__(16) uint32_t tab[FMT == kFmtIq2 ? kIq2TableWords : 4];
+    __shared__ __align__(16) uint8_t aq[kGChunkBlocks * 512];
+    __shared__ __align__(16) float xs_lds[kGRows * kGChunkBlocks];
+
+    // Item: matrix, first slot, rows.
+    uint64_t mat = a.mat;
+    uint32_t first = blockIdx.y * kGRows, count = 0, col_off = 0;
+    if (a.work) {
+        if (blockIdx.y >= *a.n_work) return;  // whole workgroup
+        const QmmWork w = a.work[blockIdx.y];
+        mat = w.mat;
+        first = w.slot;
+        count = w.count;
+        col_off = w.pad;
+    } else {
+        count = a.batch > first ? min(a.batch - first, kGRows) : 0;
+    }
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t n = lane & 15, g = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nblk_all = a.units * kBlkPerUnit;
+    const uint32_t chunk_blk = nblk_all < kGChunkBlocks ? nblk_all : kGChunkBlocks;
+    const uint32_t chunk_units = chunk_blk / kBlkPerUnit;
+    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
+    uint32_t my_n = 0;
+    if (t_begin + wave < a.tiles) {
+        const uint32_t t_end = min(a.tiles, t_begin + a.tiles_per_wg);
+        my_n = (t_end - (t_begin + wave) + kWaves - 1) / kWaves;
+    }
+    const BufRsrc rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
+    const BufRsrc d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
+    const uint32_t rec_voff = lane * 16;
+    const uint32_t d_voff = n * a.d_row * 2;
+    // Activation row of item row j (rows past `count` repeat row 0: their
+    // results are computed and dropped).
+    auto act_row = [&](uint32_t j) -> uint64_t {
+        const uint32_t s = first + (j < count ? j : 0);
+        return (a.work && a.a_row) ? a.a_row[s] : s;
+    };
+
+    uint32_t u_begin = 0;
+    uint32_t n_sub = min(a.units, chunk_units) / UPS;
+    auto tile_of = [&](uint32_t s) { return t_begin + wave + kWaves * (s / n_sub); };
+    auto first_unit = [&](uint32_t s) { return u_begin + (s % n_sub) * UPS; };
+    uint32_t steps = my_n * n_sub;
+    uint4 r0[kMaxUnitsPerStep], r1[kMaxUnitsPerStep], r2[kMaxUnitsPerStep];
+    uint32_t d0[kMaxUnitsPerStep], d1[kMaxUnitsPerStep], d2[kMaxUnitsPerStep];
+    auto load = [&](uint32_t s, uint4 (&r)[kMaxUnitsPerStep], uint32_t (&dw)[kMaxUnitsPerStep]) {
+        uint32_t rs = kBufOob, ds = kBufOob;
+        if (s < steps) {
+            const uint32_t t = tile_of(s), u = first_unit(s);
+            rs = (t * a.units + u) * 1024;
+            ds = (t * 16 * a.d_row + u * (FMT == kFmtIq2 ? 1 : 2)) * 2;
+        }
+        load_step<FMT, UPS>(rec_r, rec_voff, rs, d_r, d_voff, ds, r, dw);
+    };
+    float acc0 = 0.0f, acc1 = 0.0f;
+    uint32_t kb = 0;
+    const float* xs0 = xs_lds + (2 * g) * kGChunkBlocks;
+    const float* xs1 = xs0 + kGChunkBlocks;
+    auto compute = [&](uint32_t s, const uint4 (&r)[kMaxUnitsPerStep], const uint32_t (&dw)[kMaxUnitsPerStep]) {
+        const uint32_t ub = first_unit(s) - u_begin;
+        if (FMT == kFmtIq2)
+            step_group_iq2<UPS>(r, dw, ub, aq, xs0, xs1, tab, lane, acc0, acc1);
+        else
+            step_group_q8<UPS>(r, dw, ub, aq, xs0, xs1, lane, acc0, acc1);
+        if (s % n_sub == n_sub - 1) {
+            const uint32_t row = tile_of(s) * 16 + n;
+            if (row < a.rows) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t j = 2 * g + h;
+                    if (j < count) {
+                        float* yp = a.y + (uint64_t)(first + j) * a.y_slot + col_off + (uint64_t)row * a.y_row;
+                        const float v = h ? acc1 : acc0;
+                        *yp = (kb == 0) ? v : *yp + v;
+                    }
+                }
+            }
+            acc0 = acc1 = 0.0f;
+        }
+    };
+    // Stage chunk [kb, kb + nb) of the item's activations: thread t moves the
+    // 16-byte A words c = t + i * WG and the scales (j, b) = t + i * WG.
+    constexpr uint32_t kPer = kGStage / WG;
+    auto stage_load = [&](uint32_t kb0, uint32_t nb, uint2 (&lo)[kPer], uint2 (&hi)[kPer], float (&sc)[2]) {
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t c = threadIdx.x + i * WG;
+            const uint32_t p = c >> 6, l = c & 63, ln = l & 15, lg = l >> 4;
+            const bool ok = 2 * p < nb;
+            const int8_t* plane = (ln & 1) ? a.xl : a.xh;
+            const int8_t* src = plane + act_row(ln >> 1) * a.xq_stride + (kb0 + 2 * (ok ? p : 0)) * 32 + 8 * lg;
+            lo[i] = *reinterpret_cast<const uint2*>(src);
+            hi[i] = *reinterpret_cast<const uint2*>(src + 32);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t e = threadIdx.x + i * WG;  // < 512 = kGRows * kGChunkBlocks
+            const uint32_t j = e / kGChunkBlocks, b = e % kGChunkBlocks;
+            sc[i] = a.xs[act_row(j) * a.xs_stride + kb0 + (b < nb ? b : 0)];
+        }
+    };
+    auto stage_store = [&](uint32_t nb, const uint2 (&lo)[kPer], const uint2 (&hi)[kPer], const float (&sc)[2]) {
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t c = threadIdx.x + i * WG;
+            if (2 * (c >> 6) < nb) *reinterpret_cast<uint4*>(aq + c * 16) = make_uint4(lo[i].x, lo[i].y, hi[i].x, hi[i].y);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t e = threadIdx.x + i * WG;
+            if (e % kGChunkBlocks < nb) xs_lds[e] = sc[i];
+        }
+    };
+    {
+        uint64_t gv = 0;
+        if (FMT == kFmtIq2) gv = iq2_grid_entry();
+        uint2 lo[kPer], hi[kPer];
+        float sc[2];
+        stage_load(0, chunk_blk, lo, hi, sc);
+        __builtin_amdgcn_s_barrier();  // every wave's small loads ahead of the weights
+        load(0, r0, d0);
+        load(1, r1, d1);
+        load(2, r2, d2);
+        if (FMT == kFmtIq2) build_iq2_tables<WG>(tab, gv);
+        stage_store(chunk_blk, lo, hi, sc);
+    }
+    for (;;) {
+        lds_barrier();
+        for (uint32_t s = 0; s < steps; s += 3) {
+            compute(s, r0, d0);
+            load(s + 3, r0, d0);
+            if (s + 1 < steps) compute(s + 1, r1, d1);
+            load(s + 4, r1, d1);
+            if (s + 2 < steps) compute(s + 2, r2, d2);
+            load(s + 5, r2, d2);
+        }
+        kb += chunk_blk;
+        if (kb >= nblk_all) break;
+        const uint32_t nb = min(chunk_blk, nblk_all - kb);
+        lds_barrier();  // previous chunk's LDS no longer in use
+        u_begin = kb / kBlkPerUnit;
+        n_sub = (nb / kBlkPerUnit) / UPS;
+        steps = my_n * n_sub;
+        uint2 lo[kPer], hi[kPer];
+        float sc[2];
+        stage_load(kb, nb, lo, hi, sc);
+        load(0, r0, d0);
+        load(1, r1, d1);
+        load(2, r2, d2);
+        stage_store(nb, lo, hi, sc);
+    }
+}
+
+template <int FMT, int WG>
+const void* group_kernel_for(int ups) {
+    switch (ups) {
+        case 1: return reinterpret_cast<const void*>(&group_kernel<FMT, 1, WG>);
+        case 2: return reinterpret_cast<const void*>(&group_kernel<FMT, 2, WG>);
+        case 3: return reinterpret_cast<const void*>(&group_kernel<FMT, 3, WG>);
+        default: return reinterpret_cast<const void*>(&group_kernel<FMT, 4, WG>);
+    }
+}
+
+int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
+// Units per step: the largest of 4, 3, 2, 1 dividing both the tile's units
+// and a chunk's (Q8_0 tiles hold a multiple of 4 units).
+int group_ups(uint32_t fmt, uint32_t units) {
+    const uint32_t per_chunk = kGChunkBlocks / (fmt == kFmtIq2 ? 8 : 2);
+    const uint32_t cu = units < per_chunk ? units : per_chunk;
+    for (int u = 4; u >= 1; --u)
+        if (units % u == 0 && cu % u == 0) return u;
+    return 1;
+}
+
+int resident(const void* fn, int wg) {
+    static std::mutex mu;
+    static std::map<const void*, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(fn);
+    if (it != cache.end()) return it->second;
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, wg, 0) != hipSuccess || nb <= 0) nb = 1;
+    cache[fn] = nb;
+    return nb;
+}
+
+hipError_t launch(GroupArgs a, uint32_t fmt, uint32_t items, int num_cu, hipStream_t s) {
+    if (items == 0 || a.tiles == 0) return hipSuccess;
+    static const int wg = env_int("MMHIP_GROUP_WG", 256) == 512 ? 512 : 256;
+    const int ups = group_ups(fmt, a.units);
+    const void* fn = fmt == kFmtIq2 ? (wg == 512 ? group_kernel_for<kFmtIq2, 512>(ups) : group_kernel_for<kFmtIq2, 256>(ups))
+                                    : (wg == 512 ? group_kernel_for<kFmtQ8, 512>(ups) : group_kernel_for<kFmtQ8, 256>(ups));
+    const uint32_t waves = wg / 64;
+    const uint64_t target = (uint64_t)(num_cu > 0 ? num_cu : 256) * resident(fn, wg);
+    uint64_t tpw = ((uint64_t)items * a.tiles + target - 1) / target;
+    tpw = (tpw + waves - 1) / waves * waves;
+    if (tpw > a.tiles) tpw = (a.tiles + waves - 1) / waves * waves;
+    a.tiles_per_wg = (uint32_t)tpw;
+    const dim3 grid((unsigned)((a.tiles + tpw - 1) / tpw), items);
+    void* args[] = {&a};
+    return hipLaunchKernel(fn, grid, dim3(wg), args, 0, s);
+}
+
+GroupArgs base(const uint4* recs, const uint16_t* dvals, const TileGeom& g, const QuantAct& xq, float* y) {
+    GroupArgs a{};
+    a.recs = recs;
+    a.dvals = dvals;
+    a.rec_stride = g.rec_stride;
+    a.d_stride = g.d_stride;
+    a.d_row = (uint32_t)g.d_row;
+    a.xh = xq.hi;
+    a.xl = xq.lo;
+    a.xs = xq.scale;
+    a.xq_stride = xq.stride;
+    a.xs_stride = xq.scale_stride;
+    a.y = y;
+    a.tiles = (uint32_t)g.tiles;
+    a.units = (uint32_t)g.units;
+    a.rows = (uint32_t)g.rows;
+    return a;
+}
+
+}  // namespace
+
+hipError_t launch_group_dense(const uint4* recs, const uint16_t* dvals, const TileGeom& g, uint64_t mat,
+                              const QuantAct& xq, uint32_t batch, float* y, uint64_t y_ld, int out_layout,
+                              int num_cu, hipStream_t s) {
+    if (batch == 0) return hipSuccess;
+    GroupArgs a = base(recs, dvals, g, xq, y);
+    a.mat = mat;
+    a.batch = batch;
+    a.y_slot = out_layout == 0 ? y_ld : 1;
+    a.y_row = out_layout == 0 ? 1 : y_ld;
+    return launch(a, g.fmt, (batch + kGRows - 1) / kGRows, num_cu, s);
+}
+
+hipError_t launch_group_experts(const uint4* recs, const uint16_t* dvals, const TileGeom& g, const QuantAct& xq,
+                                const uint32_t* a_row, const QmmWork* work, const uint32_t* n_work, uint32_t max_work,
+                                float* y, uint64_t y_ld, int num_cu, hipStream_t s) {
+    GroupArgs a = base(recs, dvals, g, xq, y);
+    a.work = work;
+    a.n_work = n_work;
+    a.a_row = a_row;
+    a.y_slot = y_ld;
+    a.y_row = 1;
+    return launch(a, g.fmt, max_work, num_cu, s);
+}
+
+}  // namespace mmhip

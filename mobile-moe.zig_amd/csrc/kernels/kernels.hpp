@@ -55,7 +55,7 @@ struct GemvArgs {
 struct QmmWork {
     uint32_t mat, slot, count, pad;
 };
-constexpr uint32_t kQmmTokens = 32;  // activation rows per QMM wave
+constexpr uint32_t kQmmTokens = 8;  // activation rows per QMM work item
 
 // Raw GGUF bytes -> f32, bit-exact (dequant.zig:316-390, 632-659).
 hipError_t launch_dequant(const void* raw, uint32_t ggml_type, uint64_t n, float* out, hipStream_t s);
@@ -90,6 +90,19 @@ hipError_t launch_qmm(const uint4* recs, const uint16_t* dvals, const TileGeom& 
 hipError_t launch_qmm_grouped(const uint4* recs, const uint16_t* dvals, const TileGeom& g, const QuantAct& xq,
                               const uint32_t* a_row, const QmmWork* work, const uint32_t* n_work,
                               uint32_t max_work, float* y, uint64_t y_ld, hipStream_t s);
+
+// Quantised matmul over items of <= 8 activation rows (group.hip).
+// Dense: Y = X . W^T for `batch` rows; out_layout 0: y[b * y_ld + r],
+// 1: y[r * y_ld + b].
+hipError_t launch_group_dense(const uint4* recs, const uint16_t* dvals, const TileGeom& g, uint64_t mat,
+                              const QuantAct& xq, uint32_t batch, float* y, uint64_t y_ld, int out_layout,
+                              int num_cu, hipStream_t s);
+// Grouped: item i < *n_work multiplies activation rows a_row[slot ..
+// slot + count) (a_row null: the slots themselves) by matrix work[i].mat and
+// writes y[(slot + j) * y_ld + pad + r]. max_work bounds the grid.
+hipError_t launch_group_experts(const uint4* recs, const uint16_t* dvals, const TileGeom& g, const QuantAct& xq,
+                                const uint32_t* a_row, const QmmWork* work, const uint32_t* n_work, uint32_t max_work,
+                                float* y, uint64_t y_ld, int num_cu, hipStream_t s);
 
 // Quantises silu(g) * u per row (rows r < *n_rows, or n_rows_max when
 // n_rows is null): g = src + r * src_stride, u = g + u_off.

@@ -33,6 +33,49 @@ __device__ __forceinline__ void iq2_decode_unit(const uint4& rr, const uint32_t*
     for (int s = 0; s < 8; ++s) b[s] = (s & 1) ? iq2_bop_hi(w4[s >> 1], tab) : iq2_bop_lo(w4[s >> 1], tab);
 }
 
+// One step's records (UPS units, 1 KiB apart) and the row's scale words for
+// them. rec_soff / d_soff are the step's uniform byte offsets (kBufOob for a
+// step past the wave's end); rec_voff = lane * 16, d_voff = the row's scale
+// run. Scale runs are 16-byte aligned rows of d_row u16.
+template <int FMT, int UPS>
+__device__ __forceinline__ void load_step(BufRsrc rr, uint32_t rec_voff, uint32_t rec_soff, BufRsrc dr,
+                                          uint32_t d_voff, uint32_t d_soff, uint4 (&r)[kMaxUnitsPerStep],
+                                          uint32_t (&dw)[kMaxUnitsPerStep]) {
+#pragma unroll
+    for (int i = 0; i < UPS; ++i) r[i] = buf_load_b128<kCacheStream>(rr, rec_voff + i * 1024, rec_soff);
+    if (FMT == kFmtIq2) {
+        // Kept packed (two f16 per dword, see iq2_scale_bits): unpacking at
+        // the load would make the compiler wait for the data right there.
+        if (UPS == 8) {
+            const uint4 q = buf_load_b128<kCacheStream>(dr, d_voff, d_soff);
+            dw[0] = q.x;
+            dw[1] = q.y;
+            dw[2] = q.z;
+            dw[3] = q.w;
+        } else if (UPS == 4) {
+            const uint2 q = buf_load_b64<kCacheStream>(dr, d_voff, d_soff);
+            dw[0] = q.x;
+            dw[1] = q.y;
+        } else if (UPS == 2) {
+            dw[0] = buf_load_b32<kCacheStream>(dr, d_voff, d_soff);
+        } else {
+#pragma unroll
+            for (int i = 0; i < UPS; ++i) dw[i] = buf_load_b16<kCacheStream>(dr, d_voff + 2 * i, d_soff);
+        }
+    } else {
+        // Q8_0: one u32 (two f16) per unit; steps of 4 or 8 units start on
+        // 16-byte boundaries.
+#pragma unroll
+        for (int h = 0; h < UPS / 4; ++h) {
+            const uint4 q = buf_load_b128<kCacheStream>(dr, d_voff + 16 * h, d_soff);
+            dw[4 * h] = q.x;
+            dw[4 * h + 1] = q.y;
+            dw[4 * h + 2] = q.z;
+            dw[4 * h + 3] = q.w;
+        }
+    }
+}
+
 // f16 scale bits of unit i of a decode step: steps of 2, 4 or 8 units load
 // their scales packed two per dword, other step sizes one per word.
 template <int UPS>

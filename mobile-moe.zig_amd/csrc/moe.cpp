@@ -237,8 +237,8 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
         }
         {
             TimedLaunch tl(ctx, "moe_gateup");
-            MOE_TRY(check_hip(launch_qmm_grouped(L->gu->recs, L->gu->dvals, gg, qh, L->slot_tok, L->work_gu, L->n_work,
-                                                 route_max_work(T, E), L->y_gu, 2 * (uint64_t)I, s),
+            MOE_TRY(check_hip(launch_group_experts(L->gu->recs, L->gu->dvals, gg, qh, L->slot_tok, L->work_gu, L->n_work,
+                                                   route_max_work(T, E), L->y_gu, 2 * (uint64_t)I, ctx->num_cu, s),
                               "moe: gate/up"));
             if (sep_shared) {
                 const TileGeom& gs = L->sh_gu->geom;
@@ -246,10 +246,11 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
                     set_error(MMHIP_ERR_UNSUPPORTED, "moe: shared gate/up padding differs from the routed experts'");
                     return MMHIP_ERR_UNSUPPORTED;
                 }
-                MOE_TRY(check_hip(launch_qmm(L->sh_gu->recs, L->sh_gu->dvals, gs, 0, qh, T, L->y_sh, 2 * (uint64_t)SI, 0, s),
+                MOE_TRY(check_hip(launch_group_dense(L->sh_gu->recs, L->sh_gu->dvals, gs, 0, qh, T, L->y_sh,
+                                                     2 * (uint64_t)SI, 0, ctx->num_cu, s),
                                   "moe: shared gate"));
-                MOE_TRY(check_hip(launch_qmm(L->sh_gu->recs, L->sh_gu->dvals, gs, 1, qh, T, L->y_sh + SI,
-                                             2 * (uint64_t)SI, 0, s),
+                MOE_TRY(check_hip(launch_group_dense(L->sh_gu->recs, L->sh_gu->dvals, gs, 1, qh, T, L->y_sh + SI,
+                                                     2 * (uint64_t)SI, 0, ctx->num_cu, s),
                                   "moe: shared up"));
             }
         }
@@ -262,8 +263,8 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
         }
         {
             TimedLaunch tl(ctx, "moe_down");
-            MOE_TRY(check_hip(launch_qmm_grouped(L->dn->recs, L->dn->dvals, gd, qd, nullptr, L->work_dn, L->n_work + 1,
-                                                 route_max_work(T, E) / 2, L->eo, H, s),
+            MOE_TRY(check_hip(launch_group_experts(L->dn->recs, L->dn->dvals, gd, qd, nullptr, L->work_dn, L->n_work + 1,
+                                                   route_max_work(T, E) / 2, L->eo, H, ctx->num_cu, s),
                               "moe: down"));
             if (sep_shared) {
                 const TileGeom& gs = L->sh_dn->geom;
@@ -271,8 +272,8 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
                 MOE_TRY(check_hip(launch_quantize_silu(L->y_sh, 2 * (uint64_t)SI, SI, nullptr, T, SI,
                                                        (uint32_t)gs.cols_pad, qs, s),
                                   "moe: shared silu quantize"));
-                MOE_TRY(check_hip(launch_qmm(L->sh_dn->recs, L->sh_dn->dvals, gs, 0, qs, T,
-                                             L->eo + 4 * (uint64_t)T * H, H, 0, s),
+                MOE_TRY(check_hip(launch_group_dense(L->sh_dn->recs, L->sh_dn->dvals, gs, 0, qs, T,
+                                                     L->eo + 4 * (uint64_t)T * H, H, 0, ctx->num_cu, s),
                                   "moe: shared down"));
             }
         }
