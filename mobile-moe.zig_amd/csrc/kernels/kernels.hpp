@@ -78,19 +78,6 @@ hipError_t launch_gemv_float(const void* w, uint32_t ggml_type, uint64_t mat_str
                              const float* x, uint64_t x_stride, float* y, uint64_t y_stride,
                              uint32_t n_mats, uint32_t rows, uint32_t cols, hipStream_t s);
 
-// Batched QMM: Y = X . W^T for `batch` quantised activation rows.
-// out_layout 0: y[b * y_ld + r]; 1: y[r * y_ld + b].
-hipError_t launch_qmm(const uint4* recs, const uint16_t* dvals, const TileGeom& g, uint64_t mat,
-                      const QuantAct& xq, uint32_t batch, float* y, uint64_t y_ld, int out_layout,
-                      hipStream_t s);
-
-// Grouped QMM: work item i < *n_work multiplies activation rows
-// a_row[slot .. slot + count) (a_row null: the slots themselves) by matrix
-// work[i].mat and writes y[(slot + j) * y_ld + r]. max_work bounds the grid.
-hipError_t launch_qmm_grouped(const uint4* recs, const uint16_t* dvals, const TileGeom& g, const QuantAct& xq,
-                              const uint32_t* a_row, const QmmWork* work, const uint32_t* n_work,
-                              uint32_t max_work, float* y, uint64_t y_ld, hipStream_t s);
-
 // Quantised matmul over items of <= 8 activation rows (group.hip).
 // Dense: Y = X . W^T for `batch` rows; out_layout 0: y[b * y_ld + r],
 // 1: y[r * y_ld + b].

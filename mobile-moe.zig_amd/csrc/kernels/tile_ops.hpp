@@ -1,7 +1,8 @@
-// Per-wave tile products shared by the GEMV, QMM and MoE kernels.
+// Per-wave pieces shared by the decode GEMV and the grouped matmul: the step
+// loads of the record stream and the decode step products.
 //
 // Decode (one activation vector, A operand from the LDS A layout):
-//   units_dot_* processes up to 8 record units of one 16-row tile. Each
+//   step_dot_* processes up to 8 record units of one 16-row tile. Each
 //   32-column block is one v_mfma_i32_16x16x32_i8 with A rows 0/1 = the
 //   vector's hi/lo digits; the integer results of four consecutive blocks are
 //   gathered one per 16-lane row (gather_rows4), so every lane group scales and
@@ -9,8 +10,7 @@
 //   index % 4 == g of row n. reduce_groups() folds the four partial sums into
 //   lanes 0..15 at the end of a tile.
 //
-// Batched (tiles of 8 activation vectors, A operand from global memory):
-//   tile_mm: lane (g, n) ends with row n . vectors 2g and 2g+1 of every tile.
+// Batched products (8 activation rows per item) live in group.hip.
 #pragma once
 
 #include "device_common.hpp"
@@ -155,74 +155,6 @@ __device__ __forceinline__ void step_dot_q8(const uint4 (&r)[kMaxUnitsPerStep],
         const float d = f16_scale((dsel >> (16 * (g & 1))) & 0xFFFFu);
         const float c = (g >= 2 && !two) ? 0.0f : d * xs_g[blk0];
         acc = fmaf((float)w, c, acc);
-    }
-}
-
-// Activation source of one lane for TT vector tiles (batched products):
-// a_row[tt] is the lane's A digit row (vector tt*8 + n/2, plane n&1, offset
-// 8g) or nullptr when that vector does not exist; s0/s1[tt] are the block-
-// scale rows of vectors tt*8 + 2g and tt*8 + 2g + 1 (any valid row when
-// absent: their A rows are zero).
-template <int TT>
-struct ActTiles {
-    const int8_t* a_row[TT];
-    const float* s0[TT];
-    const float* s1[TT];
-};
-
-// Scale word of unit u in a row's scale run (layout [tile][row][unit]):
-// IQ2_XXS one f16, Q8_0 two f16 (blocks 2u, 2u+1) in one u32.
-template <int FMT>
-__device__ __forceinline__ uint32_t unit_dbits(const uint16_t* Drow, uint32_t u) {
-    if (FMT == kFmtIq2) return (uint32_t)Drow[u];
-    return reinterpret_cast<const uint32_t*>(Drow)[u];
-}
-
-// R: this lane's record pointer for unit 0 of the tile; Drow: this lane's
-// row scale run.
-template <int FMT, int TT>
-__device__ __forceinline__ void tile_mm(const uint4* __restrict__ R, const uint16_t* __restrict__ Drow,
-                                        uint32_t units, const ActTiles<TT>& act, const uint32_t* tab,
-                                        uint32_t lane, float (&acc)[TT][2]) {
-    const uint32_t g = lane >> 4;
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt) acc[tt][0] = acc[tt][1] = 0.0f;
-    for (uint32_t u = 0; u < units; ++u) {
-        const uint4 r = R[(uint64_t)u * 64];
-        const uint32_t dw = unit_dbits<FMT>(Drow, u);
-        if (FMT == kFmtIq2) {
-            const uint32_t ls = iq2_ls_all(r, g);
-            const float dq = f16_scale(dw) * 0.25f;
-            const float hdq = dq * 0.5f;
-            const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll 2
-            for (int s = 0; s < 8; ++s) {
-                const long bop = (s & 1) ? iq2_bop_hi(w4[s >> 1], tab) : iq2_bop_lo(w4[s >> 1], tab);
-                const uint32_t blk = u * 8 + s;
-                const float cw = fmaf((float)((ls >> (4 * s)) & 15u), dq, hdq);
-#pragma unroll
-                for (int tt = 0; tt < TT; ++tt) {
-                    const long aop = act.a_row[tt] ? *reinterpret_cast<const long*>(act.a_row[tt] + blk * 32) : 0;
-                    const v4i dv = mfma_i8(aop, bop);
-                    acc[tt][0] = fmaf((float)digits_combine(dv[0], dv[1]), cw * act.s0[tt][blk], acc[tt][0]);
-                    acc[tt][1] = fmaf((float)digits_combine(dv[2], dv[3]), cw * act.s1[tt][blk], acc[tt][1]);
-                }
-            }
-        } else {
-            const long bops[2] = {(long)(((uint64_t)r.y << 32) | r.x), (long)(((uint64_t)r.w << 32) | r.z)};
-            const float cws[2] = {f16_scale(dw & 0xFFFFu), f16_scale(dw >> 16)};
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const uint32_t blk = 2 * u + b;
-#pragma unroll
-                for (int tt = 0; tt < TT; ++tt) {
-                    const long aop = act.a_row[tt] ? *reinterpret_cast<const long*>(act.a_row[tt] + blk * 32) : 0;
-                    const v4i dv = mfma_i8(aop, bops[b]);
-                    acc[tt][0] = fmaf((float)digits_combine(dv[0], dv[1]), cws[b] * act.s0[tt][blk], acc[tt][0]);
-                    acc[tt][1] = fmaf((float)digits_combine(dv[2], dv[3]), cws[b] * act.s1[tt][blk], acc[tt][1]);
-                }
-            }
-        }
     }
 }
 
