@@ -85,15 +85,15 @@ __global__ void repack_iq2_kernel(const uint8_t* __restrict__ raw, uint64_t rows
             uint32_t code = (a1 >> (7 * g)) & 0x7Fu;
             if ((uint32_t)s == g) la = a1 >> 28;
             if ((uint32_t)s == 4 + g) lb = a1 >> 28;
-            uint32_t rec = (code & 7u) | ((uint32_t)(__popc(code & 15u) & 1) << 3) | (idx << 4) |
-                           (((code >> 4) & 7u) << 12);
-            w[s >> 1] |= rec << ((s & 1) ? 17 : 2);
+            const uint32_t window = (code & 7u) | ((uint32_t)(__popc(code & 15u) & 1) << 3) | (idx << 4);
+            const uint32_t hi3 = (code >> 4) & 7u;
+            w[s >> 1] |= (s & 1) ? ((window << 18) | hi3) : ((window << 3) | (hi3 << 15));
         }
         // ls of sub-block g in dwords 0,1 and of sub-block 4+g in dwords 2,3.
-        w[0] |= la & 3u;
-        w[1] |= la >> 2;
-        w[2] |= lb & 3u;
-        w[3] |= lb >> 2;
+        w[0] |= (la & 3u) << 30;
+        w[1] |= (la >> 2) << 30;
+        w[2] |= (lb & 3u) << 30;
+        w[3] |= (lb >> 2) << 30;
     }
     recs[gid] = make_uint4(w[0], w[1], w[2], w[3]);
     if (g == 0) dvals[((mat * tiles + t) * 16 + n) * d_row + j] = (uint16_t)dbits;

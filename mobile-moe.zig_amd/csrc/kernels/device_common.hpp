@@ -11,22 +11,25 @@
 //   v_mfma_i32_16x16x32_i8 (B[k][n] with k = 8g..8g+7 in lane 16g+n).
 //
 //   IQ2_XXS unit (one 256-column superblock of 16 rows, 1056 B = 16 x 66 B):
-//     recs: lane l holds 4 dwords; dword k covers sub-blocks 2k and 2k+1:
-//       bits  0.. 1  two bits of a sub-block scale ls (below)
-//       bits  2..16  record of sub-block 2k:   b012 | P<<3 | idx<<4 | hi3<<12
-//       bits 17..31  record of sub-block 2k+1 (same fields)
-//     where idx = grid index of group g, code = its 7-bit sign code,
-//     b012 = code bits 0..2, hi3 = code bits 4..6, P = parity(code bits 0..3).
-//     Dwords 0,1 carry ls of sub-block g (bits 0..1, 2..3); dwords 2,3 carry
-//     ls of sub-block 4+g. 15 information bits per record + 8 ls bits per lane
-//     = the raw format's 64 bits per sub-block-row exactly.
+//     recs: lane l holds 4 dwords; dword k covers sub-blocks 2k and 2k+1.
+//     A record is the group's grid index idx and 7-bit sign code, split as
+//     window = b012 | P<<3 | idx<<4 (12 bits) and hi3, where b012 = code
+//     bits 0..2, hi3 = code bits 4..6 and P = parity(code bits 0..3):
+//       bits  0.. 2  hi3 of sub-block 2k+1
+//       bits  3..14  window of sub-block 2k
+//       bits 15..17  hi3 of sub-block 2k
+//       bits 18..29  window of sub-block 2k+1
+//       bits 30..31  two bits of a sub-block scale ls (below)
+//     Dwords 0,1 carry ls of sub-block g, dwords 2,3 ls of sub-block 4+g.
+//     15 information bits per record + 8 ls bits per lane = the raw format's
+//     64 bits per sub-block-row exactly.
 //     d: 16 x f16, one per row.
-//   Signed int8 weights come from two 16 KiB LDS tables addressed straight
-//   from the dword:  LO[(window b012|P|idx)] = columns 0..3 (signs b0..b3,
-//   b3 = P ^ parity(b012)); HI[(window P|idx|hi3)] = columns 4..7 (signs hi3,
-//   bit 7 = P ^ parity(hi3), i.e. the ksigns parity bit). Byte addresses:
-//   rec 2k:   LO  d & 0x3FFC          HI  (d >> 3) & 0x3FFC
-//   rec 2k+1: LO  (d >> 15) & 0x3FFC  HI  (d >> 18) & 0x3FFC
+//   Signed int8 weights: one 8-byte LDS table entry per record, addressed
+//   straight from the dword (byte address d & 0x7FF8 for sub-block 2k,
+//   (d >> 15) & 0x7FF8 for 2k+1), holds all eight weights with the signs of
+//   b012, P (column 3: P ^ parity(b012)) and column 7 = P; the hi3 signs
+//   (columns 4..6, and column 7 flipped by parity(hi3): the ksigns parity
+//   bit) are applied in registers (iq2_fix_hi).
 //
 //   Q8_0 unit (two 32-column blocks of 16 rows, 1088 B = 32 x 34 B):
 //     recs: lane l holds qs[8g..8g+7] of block 2u then of block 2u+1.
@@ -50,7 +53,7 @@ constexpr int kTileRows = 16;
 constexpr int kIq2UnitCols = 256;
 constexpr int kQ8UnitCols = 64;
 constexpr float kDigitMax = 32512.0f;  // 127 * 256: hi digit stays in [-127, 127]
-constexpr int kIq2TableWords = 8192;   // LO[4096] then HI[4096], u32 each
+constexpr int kIq2TableWords = 8192;   // 4096 record entries of two u32
 // LDS A layout (decode): per 256-column group, lane (m = 0|1, g) owns a
 // 64-byte run holding the 8 A operands (8 x 8 digits) of the group's 8
 // blocks for A row m (hi/lo digits) and column group g; runs are 80 B apart so
@@ -85,6 +88,15 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+
+// Waits until all of this wave's vector memory loads have returned
+// (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their no-wait maxima).
+// A CU returns vector loads in issue order across all of its workgroups, so
+// a kernel that starts with small loads (activations, tables) and then
+// streams weights waits here before the stream: a weight stream issued
+// earlier by another workgroup on the same CU would otherwise hold those
+// small loads back behind it.
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Raw buffer loads. A load whose offset lies beyond the resource's size
 // returns zeros without a memory access, so kernels issue every load
@@ -128,23 +140,64 @@ __device__ __forceinline__ v4i mfma_i8(long a, long b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
 }
 
+// The IQ2_XXS grid (dequant.zig:148-213): 256 entries of 8 magnitudes.
+static __constant__ uint64_t c_iq2_grid[256] = {
+#include "../iq2xxs_grid.inc"
+};
+constexpr uint64_t kIq2Grid[256] = {
+#include "../iq2xxs_grid.inc"
+};
+
+// 0xFF in every byte whose bit is set in the 4-bit sign nibble m.
+__host__ __device__ constexpr uint32_t nibble_byte_mask(uint32_t m) {
+    return ((m & 1u) ? 0xFFu : 0u) | ((m & 2u) ? 0xFF00u : 0u) | ((m & 4u) ? 0xFF0000u : 0u) |
+           ((m & 8u) ? 0xFF000000u : 0u);
+}
+__host__ __device__ constexpr uint32_t parity3(uint32_t v) { return (v ^ (v >> 1) ^ (v >> 2)) & 1u; }
+// Negates the bytes selected by mask (0xFF per byte). Grid magnitudes are at
+// most 0x2B, so (b ^ 0xFF) + 1 never carries into the next byte.
+__host__ __device__ constexpr uint32_t negate_bytes(uint32_t w, uint32_t mask) {
+    return (w ^ mask) + (mask & 0x01010101u);
+}
+
+// Byte masks for the hi3 signs of a record: for hi3 = h, bit 15 - h of
+// kIq2FixS1 is hi3 bit 0 and bit 31 - h hi3 bit 1; bits 15 - h / 31 - h of
+// kIq2FixS0 are hi3 bit 2 and parity(hi3). Shifted left by h, these bits sit
+// at 15 and 31, where v_perm_b32's sign-replicating selectors (8: bit 15 of
+// the second operand, 9: its bit 31, 10/11: bits 15/31 of the first) turn
+// them into 0x00 / 0xFF bytes.
+__host__ __device__ constexpr uint32_t iq2_fix_const(bool high) {
+    uint32_t c = 0;
+    for (uint32_t h = 0; h < 8; ++h) {
+        const uint32_t a = high ? (h >> 2) & 1u : h & 1u;
+        const uint32_t b = high ? parity3(h) : (h >> 1) & 1u;
+        c |= a << (15 - h);
+        c |= b << (31 - h);
+    }
+    return c;
+}
+constexpr uint32_t kIq2FixS1 = iq2_fix_const(false);
+constexpr uint32_t kIq2FixS0 = iq2_fix_const(true);
+
+// Columns 4..7 of a record from the table's word (signs for hi3 = 0) and hi3.
+__device__ __forceinline__ uint32_t iq2_fix_hi(uint32_t w, uint32_t hi3) {
+    const uint32_t m = __builtin_amdgcn_perm(kIq2FixS0 << hi3, kIq2FixS1 << hi3, 0x0B0A0908u);
+    return negate_bytes(w, m);
+}
+
 // IQ2_XXS B operands of the two records in one tile dword.
 __device__ __forceinline__ long iq2_bop_lo(uint32_t d, const uint32_t* __restrict__ tab) {
-    const uint32_t lo = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(tab) + (d & 0x3FFCu));
-    const uint32_t hi = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(tab) + 16384u +
-                                                            ((d >> 3) & 0x3FFCu));
-    return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
+    const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(tab) + (d & 0x7FF8u));
+    return (long)(((uint64_t)iq2_fix_hi(e.y, (d >> 15) & 7u) << 32) | (uint64_t)e.x);
 }
 __device__ __forceinline__ long iq2_bop_hi(uint32_t d, const uint32_t* __restrict__ tab) {
-    const uint32_t lo = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(tab) + ((d >> 15) & 0x3FFCu));
-    const uint32_t hi = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(tab) + 16384u +
-                                                            ((d >> 18) & 0x3FFCu));
-    return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
+    const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(tab) + ((d >> 15) & 0x7FF8u));
+    return (long)(((uint64_t)iq2_fix_hi(e.y, d & 7u) << 32) | (uint64_t)e.x);
 }
 
 // ls of sub-block g (from dwords 0,1) and 4+g (dwords 2,3) of this lane.
-__device__ __forceinline__ uint32_t iq2_ls_a(const uint4& r) { return (r.x & 3u) | ((r.y & 3u) << 2); }
-__device__ __forceinline__ uint32_t iq2_ls_b(const uint4& r) { return (r.z & 3u) | ((r.w & 3u) << 2); }
+__device__ __forceinline__ uint32_t iq2_ls_a(const uint4& r) { return (r.x >> 30) | ((r.y >> 30) << 2); }
+__device__ __forceinline__ uint32_t iq2_ls_b(const uint4& r) { return (r.z >> 30) | ((r.w >> 30) << 2); }
 
 // All eight 4-bit ls values of the lane's row (nibble s = sub-block s),
 // gathered from the row's four lanes.
@@ -168,60 +221,45 @@ __device__ __forceinline__ int gather_rows4(int v0, int v1, int v2, int v3) {
     return (int)r[0];
 }
 
-// The IQ2_XXS grid (dequant.zig:148-213): 256 entries of 8 magnitudes.
-static __constant__ uint64_t c_iq2_grid[256] = {
-#include "../iq2xxs_grid.inc"
+// The 32 KiB record table (layout above), generated at compile time from
+// the grid: entry (b012 | P<<3 | idx<<4) = words (columns 0..3 of grid entry
+// idx with signs b012 and P ^ parity(b012); columns 4..7 with column 7
+// negated when P is set).
+struct Iq2Tables {
+    uint32_t w[kIq2TableWords];
 };
-
-// 0xFF in every byte whose bit is set in the 4-bit sign nibble m.
-__host__ __device__ constexpr uint32_t nibble_byte_mask(uint32_t m) {
-    return ((m & 1u) ? 0xFFu : 0u) | ((m & 2u) ? 0xFF00u : 0u) | ((m & 4u) ? 0xFF0000u : 0u) |
-           ((m & 8u) ? 0xFF000000u : 0u);
+constexpr Iq2Tables make_iq2_tables() {
+    Iq2Tables t{};
+    for (uint32_t e = 0; e < 4096; ++e) {
+        const uint32_t b012 = e & 7u, par = (e >> 3) & 1u, idx = e >> 4;
+        const uint32_t lo = (uint32_t)kIq2Grid[idx], hi = (uint32_t)(kIq2Grid[idx] >> 32);
+        t.w[2 * e] = negate_bytes(lo, nibble_byte_mask(b012 | ((par ^ parity3(b012)) << 3)));
+        t.w[2 * e + 1] = negate_bytes(hi, nibble_byte_mask(par << 3));
+    }
+    return t;
 }
-__host__ __device__ constexpr uint32_t parity3(uint32_t v) { return (v ^ (v >> 1) ^ (v >> 2)) & 1u; }
-// Negates the bytes selected by mask (0xFF per byte). Grid magnitudes are at
-// most 0x2B, so (b ^ 0xFF) + 1 never carries into the next byte.
-__device__ __forceinline__ uint32_t negate_bytes(uint32_t w, uint32_t mask) {
-    return (w ^ mask) + (mask & 0x01010101u);
-}
+static __constant__ Iq2Tables c_iq2_tables = make_iq2_tables();
 
-// Builds the 32 KiB sign/grid tables (layout above) in LDS from the 2 KiB
-// grid, for blocks of 256 or 512 threads: thread t handles grid index
-// t % 256; with 256 threads it writes LO[idx * 16 .. +15] and the 16 HI words
-// of idx, with 512 threads the first half writes LO and the second half HI.
-// iq2_grid_entry issues the thread's grid load (put it ahead of the kernel's
-// bulk loads: waits on vector loads complete in issue order);
-// build_iq2_tables writes the tables. The caller synchronises before the
-// first lookup.
-__device__ __forceinline__ uint64_t iq2_grid_entry() { return c_iq2_grid[threadIdx.x & 255u]; }
-
+// LDS copy of the tables for a workgroup of WG threads, in two halves so the
+// loads can be issued with the kernel's other small loads: thread t moves the
+// 16-byte words t + WG * i (consecutive lanes, consecutive words: no LDS bank
+// conflicts). The caller waits for the loads between the halves and
+// synchronises before the first lookup.
 template <int WG>
-__device__ __forceinline__ void build_iq2_tables(uint32_t* tab, uint64_t gv) {
-    static_assert(WG == 256 || WG == 512, "table build assumes 256 or 512 threads");
-    const uint32_t idx = threadIdx.x & 255u;
-    if (WG == 256 || threadIdx.x < 256) {
-        const uint32_t lo = (uint32_t)gv;
-        uint32_t w[16];
+struct Iq2TableCopy {
+    static constexpr int kPerThread = kIq2TableWords / 4 / WG;
+    static_assert(kIq2TableWords / 4 % WG == 0, "table copy needs WG | 2048");
+    uint4 v[kPerThread];
+    __device__ __forceinline__ void load() {
+        const BufRsrc r = make_rsrc(&c_iq2_tables, sizeof(Iq2Tables));
 #pragma unroll
-        for (uint32_t e = 0; e < 16; ++e) {
-            const uint32_t b012 = e & 7u, par = e >> 3;
-            w[e] = negate_bytes(lo, nibble_byte_mask(b012 | ((par ^ parity3(b012)) << 3)));
-        }
-        uint4* d = reinterpret_cast<uint4*>(tab + idx * 16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) d[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+        for (int i = 0; i < kPerThread; ++i) v[i] = buf_load_b128(r, (threadIdx.x + WG * i) * 16, 0);
     }
-    if (WG == 256 || threadIdx.x >= 256) {
-        const uint32_t hi = (uint32_t)(gv >> 32);
+    __device__ __forceinline__ void store(uint32_t* tab) const {
 #pragma unroll
-        for (uint32_t h3 = 0; h3 < 8; ++h3) {
-            uint2 v;
-            v.x = negate_bytes(hi, nibble_byte_mask(h3 | (parity3(h3) << 3)));
-            v.y = negate_bytes(hi, nibble_byte_mask(h3 | ((1u ^ parity3(h3)) << 3)));
-            *reinterpret_cast<uint2*>(tab + 4096 + h3 * 512 + idx * 2) = v;
-        }
+        for (int i = 0; i < kPerThread; ++i) reinterpret_cast<uint4*>(tab)[threadIdx.x + WG * i] = v[i];
     }
-}
+};
 
 // Wave-wide sum (all 64 lanes receive the result).
 __device__ __forceinline__ float wave_sum(float v) {

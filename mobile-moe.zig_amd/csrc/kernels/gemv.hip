@@ -1,12 +1,12 @@
 // Decode GEMV on gfx950.
 //
-// Quantised weights (Q8_0, IQ2_XXS): a workgroup owns one activation vector
-// (problem) and a contiguous range of 16-row tiles. It quantises the vector
-// into LDS (the A operand of every MFMA, so the separate quantisation launch
-// disappears), builds the 32 KiB IQ2_XXS sign/grid tables in LDS from the
-// 2 KiB grid, and each wave then streams its tiles' 1 KiB record units with one 128-bit load per
-// lane, through a ring of three register buffers so the next two steps'
-// loads are in flight while the current one computes. Every weight byte is read exactly once.
+// Quantised weights (Q8_0, IQ2_XXS): a workgroup of 1024 threads (one per CU)
+// owns one activation vector (problem) and a contiguous range of 16-row
+// tiles. It quantises the vector into LDS (the A operand of every MFMA, so the
+// separate quantisation launch disappears), copies the 32 KiB IQ2_XXS
+// sign/grid tables into LDS, and its 16 waves then stream equal shares of the
+// range's 1 KiB record units, one 128-bit load per lane, one step ahead of
+// the compute. Every weight byte is read exactly once.
 //
 // f32 / f16 weights (the router, matVecMulUnified's f32 branch): one
 // workgroup per output row.
@@ -23,29 +23,50 @@ namespace mmhip {
 namespace {
 
 constexpr uint32_t kChunkBlocks = 256;  // 8192 columns of activation per LDS chunk (multiple of 8)
+constexpr uint32_t kGemvMaxTiles = 64;  // tiles per workgroup (LDS row sums)
 
-// UPS = record units per step (compile-time); a tile's units in a K-chunk
-// are a whole number of steps. WG threads per workgroup.
+// Position of a decode step: tile t (within the workgroup's range) and step s
+// within the tile's part of the current K-chunk.
+struct StepPos {
+    uint32_t t, s;
+};
+
+// UPS = record units per step (compile-time); a tile's units in a K-chunk are
+// a whole number of steps. WG threads per workgroup.
+//
+// Work split: a workgroup owns one problem's tiles [t_begin, t_begin + n_tiles)
+// and, per K-chunk, its n_tiles * S steps (S steps per tile) are split into
+// kWaves contiguous, equal runs, one per wave: the wave of step j is the
+// largest w with floor(w * L / kWaves) <= j (L = n_tiles * S). A wave's run
+// covers whole tiles and at most two partial ones (its first and last).
+// Whole tiles add their row sums straight into the workgroup's LDS sums;
+// partial tiles leave theirs in the wave's edge slots (0: its first tile,
+// 1: its last), and after the chunk a combine pass adds each split tile's
+// pieces in wave order, so results do not depend on timing.
 //
 // Loads: every weight, scale and activation load goes through a buffer
 // resource and is issued unconditionally (out-of-range offsets for steps past
 // the wave's end), so each wait covers exactly the loads it needs. The
-// prologue issues the grid entry and the activation loads of all waves first,
-// then the first three steps' weights, and only then waits on the small
-// loads.
-// A ring of three register buffers keeps the next two steps' loads in flight
-// while a step computes.
+// prologue issues the table and activation loads, waits for them, fills LDS,
+// and only then starts the weight stream: a CU returns loads in issue order
+// across its waves, and a wave cannot issue while the CU's load queue is
+// full, so weights issued first would delay every wave's prologue. The
+// stream runs one step ahead (two register buffers): the CU's queue holds
+// about one step per wave, and a deeper prefetch only blocks the issuing
+// wave.
 template <int FMT, int UPS, int WG>
-__global__ __launch_bounds__(WG, (WG == 256 ? 3 : 2)) void gemv_q_kernel(GemvArgs a) {
+__global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     constexpr uint32_t kWaves = WG / 64;
     // Static LDS for the tables (known address: table offsets fold into the
-    // ds_read immediates); dynamic LDS for the activation chunk.
+    // ds_read immediates) and the row sums; dynamic LDS for the activation
+    // chunk.
     __shared__ __align__(16) uint32_t tab[FMT == kFmtIq2 ? kIq2TableWords : 4];
+    __shared__ float row_sum[kGemvMaxTiles * 16];
+    __shared__ float edge[2][kWaves * 16];
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr uint32_t kBlkPerUnit = (FMT == kFmtIq2) ? 8 : 2;
     const uint32_t nblk_all = a.units * kBlkPerUnit;
     const uint32_t chunk_blk = nblk_all < kChunkBlocks ? nblk_all : kChunkBlocks;
-    const uint32_t chunk_units = chunk_blk / kBlkPerUnit;
     int8_t* aq = reinterpret_cast<int8_t*>(smem);
     float* xs = reinterpret_cast<float*>(smem + ((chunk_blk + 7) / 8) * kAGroupBytes);
 
@@ -64,13 +85,8 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 3 : 2)) void gemv_q_kernel(GemvArg
     const float* x = a.x + x_row * a.x_stride;
     float* const y_base = a.y + y_row * a.y_stride;
     const bool silu_mul = a.silu_mul != 0;
-    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
-    // this wave's tiles: t_begin + wave + kWaves * i, i < my_n
-    uint32_t my_n = 0;
-    if (t_begin + wave < a.tiles) {
-        const uint32_t t_end = min(a.tiles, t_begin + a.tiles_per_wg);
-        my_n = (t_end - (t_begin + wave) + kWaves - 1) / kWaves;
-    }
+    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;  // < a.tiles (grid size)
+    const uint32_t n_tiles = min(a.tiles - t_begin, a.tiles_per_wg);
     const bool has_a = n < 2;
     const int8_t* a_run = aq + (n & 1) * 4 * kARun + g * kARun;  // used by lanes n < 2 only
     const float* xs_g = xs + g;
@@ -79,104 +95,127 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 3 : 2)) void gemv_q_kernel(GemvArg
     const uint32_t rec_voff = lane * 16;
     const uint32_t d_voff = n * a.d_row * 2;
 
-    // Step s of a K-chunk starting at unit u_begin: tile i = s / n_sub,
-    // units [u_begin + UPS * (s % n_sub), +UPS).
-    uint32_t u_begin = 0;
-    uint32_t n_sub = min(a.units, chunk_units) / UPS;
-    auto tile_of = [&](uint32_t s) { return t_begin + wave + kWaves * (s / n_sub); };
-    auto first_unit = [&](uint32_t s) { return u_begin + (s % n_sub) * UPS; };
-    uint32_t steps = my_n * n_sub;
-    uint4 r0[kMaxUnitsPerStep], r1[kMaxUnitsPerStep], r2[kMaxUnitsPerStep];
-    uint32_t d0[kMaxUnitsPerStep], d1[kMaxUnitsPerStep], d2[kMaxUnitsPerStep];
-    auto load = [&](uint32_t s, uint4 (&r)[kMaxUnitsPerStep], uint32_t (&dw)[kMaxUnitsPerStep]) {
+    // Per-chunk split (set by start_chunk).
+    uint32_t u_begin = 0, S = 1, L = 0, j0 = 0, j1 = 0, tf = 0;
+    auto start_chunk = [&](uint32_t nb) {
+        S = (nb / kBlkPerUnit) / UPS;
+        L = n_tiles * S;
+        j0 = wave * L / kWaves;
+        j1 = (wave + 1) * L / kWaves;
+        tf = j0 / S;
+    };
+    auto advance = [&](StepPos q) { return (q.s + 1 == S) ? StepPos{q.t + 1, 0} : StepPos{q.t, q.s + 1}; };
+    uint4 r0[kMaxUnitsPerStep], r1[kMaxUnitsPerStep];
+    uint32_t d0[kMaxUnitsPerStep], d1[kMaxUnitsPerStep];
+    auto load = [&](bool valid, StepPos q, uint4 (&r)[kMaxUnitsPerStep], uint32_t (&dw)[kMaxUnitsPerStep]) {
         uint32_t rs = kBufOob, ds = kBufOob;
-        if (s < steps) {
-            const uint32_t t = tile_of(s), u = first_unit(s);
+        if (valid) {
+            const uint32_t t = t_begin + q.t, u = u_begin + q.s * UPS;
             rs = (t * a.units + u) * 1024;
             ds = (t * 16 * a.d_row + u * (FMT == kFmtIq2 ? 1 : 2)) * 2;
         }
         load_step<FMT, UPS>(rec_r, rec_voff, rs, d_r, d_voff, ds, r, dw);
     };
     float acc = 0.0f;
-    uint32_t kb = 0;
-    // Computes step s from (r, dw); writes the tile's row sums after its last step.
-    auto compute = [&](uint32_t s, const uint4 (&r)[kMaxUnitsPerStep], const uint32_t (&dw)[kMaxUnitsPerStep]) {
-        const uint32_t ub = first_unit(s) - u_begin;  // unit index within the LDS chunk
+    bool seg_whole = true;  // the current tile segment started at the tile's first step
+    // Computes step j (position q) from (r, dw); at the end of a tile segment
+    // leaves the segment's row sums in LDS.
+    auto compute = [&](uint32_t j, StepPos q, const uint4 (&r)[kMaxUnitsPerStep],
+                       const uint32_t (&dw)[kMaxUnitsPerStep]) {
+        const uint32_t ub = q.s * UPS;  // unit index within the LDS chunk
         if (FMT == kFmtIq2)
             step_dot_iq2<UPS>(r, dw, ub, a_run, has_a, xs_g, tab, acc);
         else
             step_dot_q8<UPS>(r, dw, ub, a_run, has_a, xs_g, g, acc);
-        if (s % n_sub == n_sub - 1) {
+        const bool tile_end = q.s + 1 == S;
+        if (tile_end || j + 1 == j1) {
             const float tot = reduce_groups(acc);
             acc = 0.0f;
-            const uint32_t row = tile_of(s) * 16 + n;
-            if (lane < 16 && row < a.rows) {
-                float* yp = y_base + row;
-                *yp = (kb == 0) ? tot : *yp + tot;
+            if (lane < 16) {
+                if (seg_whole && tile_end)
+                    row_sum[q.t * 16 + n] += tot;
+                else
+                    edge[q.t == tf ? 0 : 1][wave * 16 + n] = tot;
             }
+            seg_whole = true;
         }
     };
 
     {
-        // Prologue of the first chunk (two activation passes cover 32 * WG / 4
-        // columns; longer chunks quantise the rest after the weight loads).
+        // Prologue: tables, first activation chunk, zeroed row sums.
         const uint32_t nb = chunk_blk;
         const uint32_t xb = min(a.cols, chunk_blk * 32) * 4;
         const BufRsrc x_r = make_rsrc(x, xb);
         const BufRsrc u_r = make_rsrc(x + a.x2_off, silu_mul ? xb : 0);  // zero-size: loads read 0
-        uint64_t gv = 0;
-        if (FMT == kFmtIq2) gv = iq2_grid_entry();
-        float xv0[4], xv1[4], uv0[4], uv1[4];
-        x_pass_load(x_r, 0, xv0);
-        x_pass_load(x_r, WG / 8, xv1);
-        x_pass_load(u_r, 0, uv0);
-        x_pass_load(u_r, WG / 8, uv1);
-        // A CU serves its waves' loads in issue order: the barrier (no memory
-        // fence, no wait) puts every wave's small loads ahead of the weights.
-        __builtin_amdgcn_s_barrier();
-        load(0, r0, d0);
-        load(1, r1, d1);
-        load(2, r2, d2);
-        if (FMT == kFmtIq2) build_iq2_tables<WG>(tab, gv);
-        if (silu_mul) {
-            silu_mul4(xv0, uv0);
-            silu_mul4(xv1, uv1);
-        }
-        x_pass_store(xv0, nb, 0, aq, xs);
-        x_pass_store(xv1, nb, WG / 8, aq, xs);
-        for (uint32_t b0 = 2 * (WG / 8); b0 < nb; b0 += WG / 8) {
+        Iq2TableCopy<WG> tc;
+        if (FMT == kFmtIq2) tc.load();
+        float xv[4], uv[4];
+        x_pass_load(x_r, 0, xv);
+        x_pass_load(u_r, 0, uv);
+        vm_wait_all();
+        if (FMT == kFmtIq2) tc.store(tab);
+        for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) row_sum[i] = 0.0f;
+        if (silu_mul) silu_mul4(xv, uv);
+        x_pass_store(xv, nb, 0, aq, xs);
+        for (uint32_t b0 = WG / 8; b0 < nb; b0 += WG / 8) {
             float v[4], u[4];
             x_pass_load(x_r, b0, v);
             x_pass_load(u_r, b0, u);
             if (silu_mul) silu_mul4(v, u);
             x_pass_store(v, nb, b0, aq, xs);
         }
+        start_chunk(nb);
     }
+    uint32_t kb = 0;
     for (;;) {
-        lds_barrier();
-        for (uint32_t s = 0; s < steps; s += 3) {
-            compute(s, r0, d0);
-            load(s + 3, r0, d0);
-            if (s + 1 < steps) compute(s + 1, r1, d1);
-            load(s + 4, r1, d1);
-            if (s + 2 < steps) compute(s + 2, r2, d2);
-            load(s + 5, r2, d2);
+        StepPos cur{tf, j0 - tf * S};
+        seg_whole = cur.s == 0;
+        load(j0 < j1, cur, r0, d0);
+        lds_barrier();  // activation chunk (and, first time, tables and sums) visible
+        for (uint32_t j = j0; j < j1; j += 2) {
+            StepPos nxt = advance(cur);
+            load(j + 1 < j1, nxt, r1, d1);
+            compute(j, cur, r0, d0);
+            if (j + 1 < j1) {
+                cur = nxt;
+                nxt = advance(cur);
+                load(j + 2 < j1, nxt, r0, d0);
+                compute(j + 1, cur, r1, d1);
+                cur = nxt;
+            }
+        }
+        lds_barrier();  // edge slots and whole-tile sums of this chunk written
+        // Split tiles: their pieces in wave order.
+        for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) {
+            const uint32_t t = i >> 4, rr = i & 15;
+            const uint32_t w_first = ((t * S + 1) * kWaves - 1) / L;
+            const uint32_t w_last = ((t * S + S) * kWaves - 1) / L;
+            if (w_first != w_last) {
+                float sum = 0.0f;
+                for (uint32_t w = w_first; w <= w_last; ++w) {
+                    const uint32_t aw = w * L / kWaves, bw = (w + 1) * L / kWaves;
+                    if (aw == bw) continue;  // empty run
+                    sum += edge[aw / S == t ? 0 : 1][w * 16 + rr];
+                }
+                row_sum[i] += sum;
+            }
         }
         kb += chunk_blk;
         if (kb >= nblk_all) break;
         // Next K-chunk (activations longer than one LDS chunk).
         const uint32_t nb = min(chunk_blk, nblk_all - kb);
-        lds_barrier();  // previous chunk's LDS no longer in use
+        lds_barrier();  // previous chunk's LDS (activations, edge slots) no longer in use
         u_begin = kb / kBlkPerUnit;
-        n_sub = (nb / kBlkPerUnit) / UPS;
-        steps = my_n * n_sub;
-        load(0, r0, d0);
-        load(1, r1, d1);
-        load(2, r2, d2);
         const uint32_t c0 = kb * 32;
         const uint32_t cb = (a.cols > c0 ? min(a.cols - c0, nb * 32) : 0) * 4;
         quantize_to_lds<WG>(make_rsrc(x + c0, cb), make_rsrc(x + a.x2_off + c0, silu_mul ? cb : 0), silu_mul, nb, aq,
                             xs);
+        start_chunk(nb);
+    }
+    lds_barrier();  // all row sums final
+    for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) {
+        const uint32_t row = (t_begin + (i >> 4)) * 16 + (i & 15);
+        if (row < a.rows) y_base[row] = row_sum[i];
     }
 }
 
@@ -288,33 +327,40 @@ static int resident_per_cu(const void* fn, int wg, size_t lds) {
     return nb;
 }
 
+template <int FMT>
+static const void* kernel_for_wg(int wg, int ups) {
+    if (wg == 256) return kernel_for<FMT, 256>(ups);
+    if (wg == 512) return kernel_for<FMT, 512>(ups);
+    return kernel_for<FMT, 1024>(ups);
+}
+
 hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStream_t s) {
     if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
     GemvArgs a = a_in;
     // Tuning knobs (defaults measured on MI355X): MMHIP_GEMV_WG threads per
-    // workgroup (256 | 512), MMHIP_GEMV_MAX_UPS caps record units per step,
-    // MMHIP_GEMV_WG_PER_CU overrides the resident workgroups per CU that the
-    // grid is sized for (default: the occupancy the kernel reaches).
-    static const int wg = env_int("MMHIP_GEMV_WG", 256) == 512 ? 512 : 256;
+    // workgroup (256 | 512 | 1024), MMHIP_GEMV_MAX_UPS caps record units per
+    // step, MMHIP_GEMV_WG_PER_CU overrides the resident workgroups per CU that
+    // the grid is sized for (default: the occupancy the kernel reaches).
+    static const int wg_env = env_int("MMHIP_GEMV_WG", 1024);
+    static const int wg = (wg_env == 256 || wg_env == 512) ? wg_env : 1024;
     static const int cap_env = env_int("MMHIP_GEMV_MAX_UPS", 0);
-    // Steps above 4 units exceed the register budget of 3 waves per SIMD
-    // (168 VGPRs with two record buffers) and spill.
+    // Steps above 4 units exceed the register budget of 4 waves per SIMD
+    // (128 VGPRs with two record buffers) and spill.
     const int cap = cap_env > 0 ? cap_env : 4;
     static const int wg_per_cu_env = env_int("MMHIP_GEMV_WG_PER_CU", 0);
     int ups = pick_ups(fmt, a.units);
     if (ups == 0) return hipErrorInvalidValue;
     while (ups > cap && ups % 2 == 0 && (fmt == kFmtIq2 || ups > 4)) ups /= 2;
-    const void* fn = fmt == kFmtIq2 ? (wg == 512 ? kernel_for<kFmtIq2, 512>(ups) : kernel_for<kFmtIq2, 256>(ups))
-                                    : (wg == 512 ? kernel_for<kFmtQ8, 512>(ups) : kernel_for<kFmtQ8, 256>(ups));
+    const void* fn = fmt == kFmtIq2 ? kernel_for_wg<kFmtIq2>(wg, ups) : kernel_for_wg<kFmtQ8>(wg, ups);
     const size_t lds = gemv_q_lds_bytes(fmt, a.units);
     const int wg_per_cu = wg_per_cu_env > 0 ? wg_per_cu_env : resident_per_cu(fn, wg, lds);
-    const uint32_t waves = wg / 64;
+    // Tiles per workgroup: the problems' tiles spread over every resident
+    // workgroup slot of the device, at most kGemvMaxTiles (the LDS row sums).
     const uint64_t total_tiles = (uint64_t)a.n_probs * a.tiles;
     const uint64_t target_wgs = (uint64_t)(num_cu > 0 ? num_cu : 256) * wg_per_cu;
-    uint64_t tpw = (total_tiles + target_wgs - 1) / target_wgs;  // tiles per WG
-    tpw = (tpw + waves - 1) / waves * waves;
-    if (tpw < waves) tpw = waves;
-    if (tpw > a.tiles) tpw = (a.tiles + waves - 1) / waves * waves;
+    uint64_t tpw = (total_tiles + target_wgs - 1) / target_wgs;
+    if (tpw > kGemvMaxTiles) tpw = kGemvMaxTiles;
+    if (tpw > a.tiles) tpw = a.tiles;
     a.tiles_per_wg = (uint32_t)tpw;
     dim3 grid((unsigned)((a.tiles + tpw - 1) / tpw), a.n_probs);
     void* args[] = {&a};

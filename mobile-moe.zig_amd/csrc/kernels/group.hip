@@ -13,7 +13,7 @@
 // cross-lane reduction is needed.
 //
 // Streaming is the decode GEMV's: unconditional buffer loads, a ring of three
-// register buffers, an LDS-only barrier, tables built from the grid.
+// register buffers, an LDS-only barrier, tables copied into LDS.
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "tile_ops.hpp"
@@ -239,17 +239,19 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
         }
     };
     {
-        uint64_t gv = 0;
-        if (FMT == kFmtIq2) gv = iq2_grid_entry();
+        // Small loads first and waited for: a CU returns loads in issue order
+        // across its waves, so weights issued first would hold them back.
+        Iq2TableCopy<WG> tc;
+        if (FMT == kFmtIq2) tc.load();
         uint2 lo[kPer], hi[kPer];
         float sc[2];
         stage_load(0, chunk_blk, lo, hi, sc);
-        __builtin_amdgcn_s_barrier();  // every wave's small loads ahead of the weights
+        vm_wait_all();
+        if (FMT == kFmtIq2) tc.store(tab);
+        stage_store(chunk_blk, lo, hi, sc);
         load(0, r0, d0);
         load(1, r1, d1);
         load(2, r2, d2);
-        if (FMT == kFmtIq2) build_iq2_tables<WG>(tab, gv);
-        stage_store(chunk_blk, lo, hi, sc);
     }
     for (;;) {
         lds_barrier();
