@@ -9,9 +9,9 @@ Weights rotate over distinct device copies (> 1 GiB, several times the
 256 MiB Infinity Cache), so every step streams its weights from HBM.
 
 Also reported:
-  roofline      the GEMV kernel: algorithmic bytes per launch / its mean
-                duration, from one pair of HIP events around back-to-back
-                launches of each shape on the library's stream, against the
+  roofline      the GEMV kernel: algorithmic bytes per launch / its duration,
+                the median over alternating blocks of back-to-back launches
+                of each shape (HIP event pairs on the library's stream), against the
                 8 TB/s HBM peak; `traffic` is the HBM bytes per launch from the
                 FETCH_SIZE / WRITE_SIZE counter runs summarised in
                 profiles/gemv_iq2_traffic.txt (null when that file is absent)
@@ -125,10 +125,17 @@ def gemv_section(ctx, ev, fmt, steps, warmup, pool_gib, rng):
         down(i)
     ctx.synchronize()
     dt = time.perf_counter() - t0
-    # Kernel durations: one event pair around back-to-back launches of a shape.
+    # Kernel durations: event pairs around blocks of back-to-back launches of
+    # one shape, the shapes' blocks alternating; the median block gives the
+    # per-launch time (the device's clock state drifts over a long run, and a
+    # single block can land in a slow stretch).
     stream = ctx.stream
-    g_ms = ev.time_ms(stream, lambda: [gate(i) for i in range(steps)]) / steps
-    d_ms = ev.time_ms(stream, lambda: [down(i) for i in range(steps)]) / steps
+    blocks, per = 7, max(10, steps // 4)
+    g_blk, d_blk = [], []
+    for b in range(blocks):
+        g_blk.append(ev.time_ms(stream, lambda: [gate(b * per + i) for i in range(per)]) / per)
+        d_blk.append(ev.time_ms(stream, lambda: [down(b * per + i) for i in range(per)]) / per)
+    g_ms, d_ms = float(np.median(g_blk)), float(np.median(d_blk))
     for g, d in sets:
         g.free()
         d.free()

@@ -253,7 +253,7 @@ int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t 
     }
     const TileGeom& g = w->geom;
     (void)qscratch;
-    GemvArgs a;
+    GemvArgs a{};
     a.recs = w->recs;
     a.dvals = w->dvals;
     a.rec_stride = g.rec_stride;

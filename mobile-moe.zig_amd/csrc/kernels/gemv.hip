@@ -12,6 +12,7 @@
 // workgroup per output row.
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "route_ops.hpp"
 #include "tile_ops.hpp"
 
 #include <cstdlib>
@@ -24,6 +25,45 @@ namespace {
 
 constexpr uint32_t kChunkBlocks = 256;  // 8192 columns of activation per LDS chunk (multiple of 8)
 constexpr uint32_t kGemvMaxTiles = 64;  // tiles per workgroup (LDS row sums)
+
+// The routing outputs of a decode call (the single-token branch of the
+// routing kernel): route ids / weights, statistics, slots in route order,
+// the shared slot, and the down problem list. One thread.
+__device__ __forceinline__ void decode_route_outputs(const RouteArgs& a, const TokenRoute& tr) {
+    const uint32_t E = a.n_experts, k = a.k;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i) {
+        if (a.route_ids) a.route_ids[i] = i < k ? tr.ids[i] : 0xFFFFFFFFu;
+        if (a.route_w) a.route_w[i] = i < k ? tr.w[i] : 0.0f;
+        a.assign_w[i] = ((tr.act >> i) & 1u) ? tr.w[i] : 0.0f;
+        a.assign_slot[i] = -1;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i)
+        if (i < k) atomicAdd(a.counts + tr.ids[i], 1ull);  // stats.record
+    a.deferred[0] = tr.deferred;
+    a.shared_slot[0] = a.shared ? 4 : -1;
+    a.slot_tok[4] = 0;
+    uint32_t s = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i) {
+        if (i >= k || !((tr.act >> i) & 1u)) continue;
+        a.assign_slot[i] = (int32_t)s;
+        a.slot_tok[s] = 0;
+        a.gemv_gu[2 * s] = make_uint4(tr.ids[i], 0, 2 * s, 0);
+        a.gemv_gu[2 * s + 1] = make_uint4(E + tr.ids[i], 0, 2 * s + 1, 0);
+        a.gemv_dn[s] = make_uint4(tr.ids[i], s, s, 0);
+        ++s;
+    }
+    uint32_t n_gu = 2 * s, n_dn = s;
+    if (a.shared && a.shared_merged) {
+        a.gemv_gu[n_gu++] = make_uint4(2 * E, 0, 8, 0);
+        a.gemv_gu[n_gu++] = make_uint4(2 * E + 1, 0, 9, 0);
+        a.gemv_dn[n_dn++] = make_uint4(E, 4, 4, 0);
+    }
+    a.n_gemv[0] = n_gu;
+    a.n_gemv[1] = n_dn;
+}
 
 // Position of a decode step: tile t (within the workgroup's range) and step s
 // within the tile's part of the current K-chunk.
@@ -54,9 +94,10 @@ struct StepPos {
 // stream runs one step ahead (two register buffers): the CU's queue holds
 // about one step per wave, and a deeper prefetch only blocks the issuing
 // wave.
-template <int FMT, int UPS, int WG>
+template <int FMT, int UPS, int WG, int DEPTH, bool ROUTE>
 __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     constexpr uint32_t kWaves = WG / 64;
+    constexpr int kRing = DEPTH + 1;  // register buffers: the step computing + DEPTH in flight
     // Static LDS for the tables (known address: table offsets fold into the
     // ds_read immediates) and the row sums; dynamic LDS for the activation
     // chunk.
@@ -74,13 +115,36 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t p = blockIdx.y;
-    if (a.n_active && p >= *a.n_active) return;  // whole workgroup: problem not in this call's list
     uint64_t mat = a.first_mat + p, x_row = p, y_row = p;
-    if (a.probs) {
-        const uint4 d = a.probs[p];
-        mat = d.x;
-        x_row = d.y;
-        y_row = d.z;
+    if constexpr (ROUTE) {
+        // Every wave routes the token (same result); the problem follows.
+        const TokenRoute tr = route_token(a.route, 0);
+        if (p == 0 && blockIdx.x == 0 && threadIdx.x == 0) decode_route_outputs(a.route, tr);
+        const uint32_t E = a.route.n_experts;
+        uint32_t n_act = 0, e_sel = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < kMaxK; ++i)
+            if (i < a.route.k && ((tr.act >> i) & 1u)) {
+                if (n_act == p >> 1) e_sel = tr.ids[i];
+                ++n_act;
+            }
+        x_row = 0;
+        if (p < 2 * n_act) {
+            mat = (p & 1u) ? E + e_sel : e_sel;
+        } else if (a.route.shared && a.route.shared_merged && p < 2 * n_act + 2) {
+            mat = 2 * E + (p - 2 * n_act);
+            y_row = 8 + (p - 2 * n_act);
+        } else {
+            return;  // whole workgroup: no such problem this call
+        }
+    } else {
+        if (a.n_active && p >= *a.n_active) return;  // whole workgroup: problem not in this call's list
+        if (a.probs) {
+            const uint4 d = a.probs[p];
+            mat = d.x;
+            x_row = d.y;
+            y_row = d.z;
+        }
     }
     const float* x = a.x + x_row * a.x_stride;
     float* const y_base = a.y + y_row * a.y_stride;
@@ -105,8 +169,8 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
         tf = j0 / S;
     };
     auto advance = [&](StepPos q) { return (q.s + 1 == S) ? StepPos{q.t + 1, 0} : StepPos{q.t, q.s + 1}; };
-    uint4 r0[kMaxUnitsPerStep], r1[kMaxUnitsPerStep];
-    uint32_t d0[kMaxUnitsPerStep], d1[kMaxUnitsPerStep];
+    uint4 rb[kRing][kMaxUnitsPerStep];
+    uint32_t db[kRing][kMaxUnitsPerStep];
     auto load = [&](bool valid, StepPos q, uint4 (&r)[kMaxUnitsPerStep], uint32_t (&dw)[kMaxUnitsPerStep]) {
         uint32_t rs = kBufOob, ds = kBufOob;
         if (valid) {
@@ -118,6 +182,18 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     };
     float acc = 0.0f;
     bool seg_whole = true;  // the current tile segment started at the tile's first step
+    StepPos cur{0, 0}, nxt{0, 0};  // the step to compute, the next to load
+    // Issues the first DEPTH steps of the current chunk.
+    auto issue_first = [&]() {
+        cur = StepPos{tf, j0 - tf * S};
+        nxt = cur;
+        seg_whole = cur.s == 0;
+#pragma unroll
+        for (int q = 0; q < DEPTH; ++q) {
+            load(j0 + q < j1, nxt, rb[q], db[q]);
+            nxt = advance(nxt);
+        }
+    };
     // Computes step j (position q) from (r, dw); at the end of a tile segment
     // leaves the segment's row sums in LDS.
     auto compute = [&](uint32_t j, StepPos q, const uint4 (&r)[kMaxUnitsPerStep],
@@ -153,6 +229,12 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
         x_pass_load(x_r, 0, xv);
         x_pass_load(u_r, 0, uv);
         vm_wait_all();
+        // When one pass covers the chunk, no activation load follows, and the
+        // first weight steps go out now so that their latency overlaps the LDS
+        // fill below (a later activation load would wait behind them).
+        start_chunk(nb);
+        const bool early = nb <= WG / 8;
+        if (early) issue_first();
         if (FMT == kFmtIq2) tc.store(tab);
         for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) row_sum[i] = 0.0f;
         if (silu_mul) silu_mul4(xv, uv);
@@ -164,24 +246,22 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
             if (silu_mul) silu_mul4(v, u);
             x_pass_store(v, nb, b0, aq, xs);
         }
-        start_chunk(nb);
+        if (!early) issue_first();
     }
     uint32_t kb = 0;
     for (;;) {
-        StepPos cur{tf, j0 - tf * S};
-        seg_whole = cur.s == 0;
-        load(j0 < j1, cur, r0, d0);
         lds_barrier();  // activation chunk (and, first time, tables and sums) visible
-        for (uint32_t j = j0; j < j1; j += 2) {
-            StepPos nxt = advance(cur);
-            load(j + 1 < j1, nxt, r1, d1);
-            compute(j, cur, r0, d0);
-            if (j + 1 < j1) {
-                cur = nxt;
-                nxt = advance(cur);
-                load(j + 2 < j1, nxt, r0, d0);
-                compute(j + 1, cur, r1, d1);
-                cur = nxt;
+        for (uint32_t j = j0; j < j1; j += kRing) {
+            // Buffer q holds step j + q; the load of step j + q + DEPTH goes
+            // into the buffer of step j + q - 1, computed just before.
+#pragma unroll
+            for (int q = 0; q < kRing; ++q) {
+                if (j + q < j1) {
+                    load(j + q + DEPTH < j1, nxt, rb[(q + DEPTH) % kRing], db[(q + DEPTH) % kRing]);
+                    nxt = advance(nxt);
+                    compute(j + q, cur, rb[q], db[q]);
+                    cur = advance(cur);
+                }
             }
         }
         lds_barrier();  // edge slots and whole-tile sums of this chunk written
@@ -211,6 +291,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
         quantize_to_lds<WG>(make_rsrc(x + c0, cb), make_rsrc(x + a.x2_off + c0, silu_mul ? cb : 0), silu_mul, nb, aq,
                             xs);
         start_chunk(nb);
+        issue_first();
     }
     lds_barrier();  // all row sums final
     for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) {
@@ -293,17 +374,17 @@ static int pick_ups(uint32_t fmt, uint32_t units) {
     return 0;
 }
 
-template <int FMT, int WG>
+template <int FMT, int WG, int DEPTH, bool ROUTE>
 static const void* kernel_for(int ups) {
     switch (ups) {
-        case 1: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 1, WG>);
-        case 2: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 2, WG>);
-        case 3: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 3, WG>);
-        case 4: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 4, WG>);
-        case 5: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 5, WG>);
-        case 6: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 6, WG>);
-        case 7: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 7, WG>);
-        default: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 8, WG>);
+        case 1: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 1, WG, DEPTH, ROUTE>);
+        case 2: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 2, WG, DEPTH, ROUTE>);
+        case 3: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 3, WG, DEPTH, ROUTE>);
+        case 4: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 4, WG, DEPTH, ROUTE>);
+        case 5: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 5, WG, DEPTH, ROUTE>);
+        case 6: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 6, WG, DEPTH, ROUTE>);
+        case 7: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 7, WG, DEPTH, ROUTE>);
+        default: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 8, WG, DEPTH, ROUTE>);
     }
 }
 
@@ -327,33 +408,55 @@ static int resident_per_cu(const void* fn, int wg, size_t lds) {
     return nb;
 }
 
-template <int FMT>
+template <int FMT, int DEPTH>
 static const void* kernel_for_wg(int wg, int ups) {
-    if (wg == 256) return kernel_for<FMT, 256>(ups);
-    if (wg == 512) return kernel_for<FMT, 512>(ups);
-    return kernel_for<FMT, 1024>(ups);
+    if (wg == 256) return kernel_for<FMT, 256, DEPTH, false>(ups);
+    return kernel_for<FMT, 1024, DEPTH, false>(ups);
 }
 
 hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStream_t s) {
     if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
     GemvArgs a = a_in;
-    // Tuning knobs (defaults measured on MI355X): MMHIP_GEMV_WG threads per
-    // workgroup (256 | 512 | 1024), MMHIP_GEMV_MAX_UPS caps record units per
-    // step, MMHIP_GEMV_WG_PER_CU overrides the resident workgroups per CU that
-    // the grid is sized for (default: the occupancy the kernel reaches).
-    static const int wg_env = env_int("MMHIP_GEMV_WG", 1024);
-    static const int wg = (wg_env == 256 || wg_env == 512) ? wg_env : 1024;
+    // Per-format defaults, measured on MI355X with 64-expert batches:
+    //   IQ2_XXS (decode-bound): 1024 threads, one workgroup per CU (16 waves
+    //     to hide the table and MFMA latencies), one step in flight (a step
+    //     computes long enough to cover the load latency);
+    //   Q8_0 (HBM-bound): 256 threads, one workgroup per CU, two steps in
+    //     flight: four long streams per CU keep fewer requests outstanding
+    //     and reach a higher HBM rate than sixteen.
+    // Overrides: MMHIP_GEMV_WG (256 | 1024), MMHIP_GEMV_MAX_UPS (record units
+    // per step), MMHIP_GEMV_DEPTH (steps in flight, 1..3),
+    // MMHIP_GEMV_WG_PER_CU (workgroups per CU the grid is sized for).
+    static const int wg_env = env_int("MMHIP_GEMV_WG", 0);
     static const int cap_env = env_int("MMHIP_GEMV_MAX_UPS", 0);
+    static const int depth_env = env_int("MMHIP_GEMV_DEPTH", 0);
+    static const int wg_per_cu_env = env_int("MMHIP_GEMV_WG_PER_CU", 0);
+    const bool iq2 = fmt == kFmtIq2;
+    int wg = (wg_env == 256 || wg_env == 1024) ? wg_env : (iq2 ? 1024 : 256);
     // Steps above 4 units exceed the register budget of 4 waves per SIMD
     // (128 VGPRs with two record buffers) and spill.
-    const int cap = cap_env > 0 ? cap_env : 4;
-    static const int wg_per_cu_env = env_int("MMHIP_GEMV_WG_PER_CU", 0);
+    // The routing variant (decode gate/up) keeps IQ2_XXS steps at 2 units:
+    // its prologue's registers would make 4-unit steps spill.
+    const int cap = (a.route_decode && iq2) ? 2 : (cap_env > 0 ? cap_env : 4);
     int ups = pick_ups(fmt, a.units);
     if (ups == 0) return hipErrorInvalidValue;
-    while (ups > cap && ups % 2 == 0 && (fmt == kFmtIq2 || ups > 4)) ups /= 2;
-    const void* fn = fmt == kFmtIq2 ? kernel_for_wg<kFmtIq2>(wg, ups) : kernel_for_wg<kFmtQ8>(wg, ups);
+    while (ups > cap && ups % 2 == 0 && (iq2 || ups > 4)) ups /= 2;
+    int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : (iq2 ? 1 : 2);
+    const void* fn;
+    if (a.route_decode) {
+        // Decode gate/up with routing in the kernel: the default shapes only.
+        wg = iq2 ? 1024 : 256;
+        depth = iq2 ? 1 : 2;
+        fn = iq2 ? kernel_for<kFmtIq2, 1024, 1, true>(ups) : kernel_for<kFmtQ8, 256, 2, true>(ups);
+    } else if (iq2) {
+        fn = depth == 1 ? kernel_for_wg<kFmtIq2, 1>(wg, ups) : kernel_for_wg<kFmtIq2, 2>(wg, ups);
+    } else {
+        fn = depth == 1   ? kernel_for_wg<kFmtQ8, 1>(wg, ups)
+             : depth == 3 ? kernel_for_wg<kFmtQ8, 3>(wg, ups)
+                          : kernel_for_wg<kFmtQ8, 2>(wg, ups);
+    }
     const size_t lds = gemv_q_lds_bytes(fmt, a.units);
-    const int wg_per_cu = wg_per_cu_env > 0 ? wg_per_cu_env : resident_per_cu(fn, wg, lds);
+    const int wg_per_cu = wg_per_cu_env > 0 ? wg_per_cu_env : (iq2 ? resident_per_cu(fn, wg, lds) : 1);
     // Tiles per workgroup: the problems' tiles spread over every resident
     // workgroup slot of the device, at most kGemvMaxTiles (the LDS row sums).
     const uint64_t total_tiles = (uint64_t)a.n_probs * a.tiles;

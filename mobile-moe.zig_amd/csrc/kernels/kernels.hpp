@@ -32,6 +32,38 @@ struct QuantAct {
     uint64_t scale_stride; // scales between vectors (= stride / 32)
 };
 
+// One item of a grouped (expert-sorted) QMM: rows [slot, slot + count) of the
+// activation list against matrix `mat`; count <= kQmmTokens.
+struct QmmWork {
+    uint32_t mat, slot, count, pad;
+};
+constexpr uint32_t kQmmTokens = 8;  // activation rows per QMM work item
+
+struct RouteArgs {
+    const float* scores;        // [n_tokens][n_experts]
+    uint32_t n_tokens, n_experts;
+    uint32_t k;                 // min(active_expert_limit, 4), >= 1
+    int32_t level;              // throttle level 0..3
+    float scale;                // getRoutedScalingFactor
+    uint32_t shared;            // 1: the layer has a shared expert
+    uint32_t shared_merged;     // 1: shared gate/up are matrices 2E, 2E+1 and shared down is matrix E
+    unsigned long long* counts; // ExpertStats.counts of the layer [n_experts]
+    uint32_t* route_ids;        // [n_tokens][4] or null
+    float* route_w;             // [n_tokens][4] or null
+    int32_t* assign_slot;       // [n_tokens][4]: slot of (t, i), -1 = none (skipped or i >= k)
+    float* assign_w;            // [n_tokens][4]
+    int32_t* shared_slot;       // [n_tokens]: slot of the shared expert, -1 = none
+    uint32_t* deferred;         // [n_tokens]
+    uint32_t* slot_tok;         // [5 n_tokens]: token of each slot
+    uint4* gemv_gu;             // n_tokens == 1: {matrix, 0, 2 slot + (0 gate | 1 up), 0}
+    uint4* gemv_dn;             //                {matrix, slot, slot, 0}
+    uint32_t* n_gemv;           // [2]: active entries of gemv_gu, gemv_dn
+    QmmWork* work_gu;           // n_tokens > 1: grouped items (gate col 0, up col inter)
+    QmmWork* work_dn;
+    uint32_t* n_work;           // [2]: active items of work_gu, work_dn
+    uint32_t inter;             // routed expert width (up column offset)
+};
+
 struct GemvArgs {
     const uint4* recs;
     const uint16_t* dvals;
@@ -48,14 +80,17 @@ struct GemvArgs {
     const uint32_t* n_active;       // device: problems p >= *n_active do nothing, or null
     uint32_t n_probs, tiles, units, rows, cols;
     uint32_t tiles_per_wg;          // set by launch_gemv_q
+    // Decode gate/up (route_decode = 1): the problems come from routing the
+    // single token's scores (route.scores) inside the kernel, not from probs /
+    // n_active: problem 2s + h is half h (0 gate, 1 up) of the s-th computed
+    // assignment (matrix id or E + id, y row 2s + h), then the merged shared
+    // expert's gate / up (matrices 2E, 2E+1, y rows 8, 9). Workgroup (0, 0)
+    // also writes the routing outputs the later kernels read (route ids and
+    // weights, statistics, slots, the down problem list).
+    RouteArgs route{};
+    uint32_t route_decode = 0;
 };
 
-// One item of a grouped (expert-sorted) QMM: rows [slot, slot + count) of the
-// activation list against matrix `mat`; count <= kQmmTokens.
-struct QmmWork {
-    uint32_t mat, slot, count, pad;
-};
-constexpr uint32_t kQmmTokens = 8;  // activation rows per QMM work item
 
 // Raw GGUF bytes -> f32, bit-exact (dequant.zig:316-390, 632-659).
 hipError_t launch_dequant(const void* raw, uint32_t ggml_type, uint64_t n, float* out, hipStream_t s);
@@ -107,30 +142,7 @@ hipError_t launch_quantize_silu(const float* src, uint64_t src_stride, uint64_t 
 
 // Scheduler.route (scheduler.zig:169-262) for every token on the device, plus
 // the problem lists of the expert products.
-struct RouteArgs {
-    const float* scores;        // [n_tokens][n_experts]
-    uint32_t n_tokens, n_experts;
-    uint32_t k;                 // min(active_expert_limit, 4), >= 1
-    int32_t level;              // throttle level 0..3
-    float scale;                // getRoutedScalingFactor
-    uint32_t shared;            // 1: the layer has a shared expert
-    uint32_t shared_merged;     // 1: shared gate/up are matrices 2E, 2E+1 and shared down is matrix E
-    unsigned long long* counts; // ExpertStats.counts of the layer [n_experts]
-    uint32_t* route_ids;        // [n_tokens][4] or null
-    float* route_w;             // [n_tokens][4] or null
-    int32_t* assign_slot;       // [n_tokens][4]: slot of (t, i), -1 = none (skipped or i >= k)
-    float* assign_w;            // [n_tokens][4]
-    int32_t* shared_slot;       // [n_tokens]: slot of the shared expert, -1 = none
-    uint32_t* deferred;         // [n_tokens]
-    uint32_t* slot_tok;         // [5 n_tokens]: token of each slot
-    uint4* gemv_gu;             // n_tokens == 1: {matrix, 0, 2 slot + (0 gate | 1 up), 0}
-    uint4* gemv_dn;             //                {matrix, slot, slot, 0}
-    uint32_t* n_gemv;           // [2]: active entries of gemv_gu, gemv_dn
-    QmmWork* work_gu;           // n_tokens > 1: grouped items (gate col 0, up col inter)
-    QmmWork* work_dn;
-    uint32_t* n_work;           // [2]: active items of work_gu, work_dn
-    uint32_t inter;             // routed expert width (up column offset)
-};
+
 hipError_t launch_route(const RouteArgs& a, hipStream_t s);
 // Upper bound of the grouped items per list for T tokens and E experts.
 uint32_t route_max_work(uint32_t n_tokens, uint32_t n_experts);

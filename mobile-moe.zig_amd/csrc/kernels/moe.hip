@@ -14,6 +14,7 @@
 // deferral bias, with products and sums rounded separately as on the CPU.
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "route_ops.hpp"
 
 namespace mmhip {
 
@@ -22,183 +23,43 @@ namespace {
 constexpr int kRouteThreads = 1024;  // 16 waves; one wave per token at a time
 constexpr int kMaxTokens = 256;      // MMHIP_MOE_MAX_TOKENS
 constexpr int kMaxExperts = 256;
-constexpr int kMaxK = 4;
 
-// The size-k min-heap of math.topK (math.zig:130-193) for k <= 4, held in
-// registers: every position is a compile-time index, so siftDownMin's
-// comparisons (children 2p+1, 2p+2 of parent p, strict <, left first) are
-// spelled out for the only parents a heap of <= 4 entries has: 0 and 1.
-struct Heap4 {
-    uint32_t i0, i1, i2, i3;
-    float s0, s1, s2, s3;
-    __device__ void swap01() {
-        uint32_t ti = i0; i0 = i1; i1 = ti;
-        float ts = s0; s0 = s1; s1 = ts;
-    }
-    __device__ void swap02() {
-        uint32_t ti = i0; i0 = i2; i2 = ti;
-        float ts = s0; s0 = s2; s2 = ts;
-    }
-    __device__ void swap13() {
-        uint32_t ti = i1; i1 = i3; i3 = ti;
-        float ts = s1; s1 = s3; s3 = ts;
-    }
-    // siftDownMin(start = 1, end): the only child of position 1 is 3.
-    __device__ void sift1(uint32_t end) {
-        if (3 < end && s3 < s1) swap13();
-    }
-    // siftDownMin(start = 0, end).
-    __device__ void sift0(uint32_t end) {
-        uint32_t smallest = 0;
-        float sm = s0;
-        if (1 < end && s1 < sm) {
-            smallest = 1;
-            sm = s1;
-        }
-        if (2 < end && s2 < sm) smallest = 2;
-        if (smallest == 1) {
-            swap01();
-            sift1(end);
-        } else if (smallest == 2) {
-            swap02();  // position 2 has no children below 4
-        }
-    }
+// LDS of the routing pass (one workgroup of kRouteThreads threads).
+struct RouteLds {
+    uint32_t ids[kMaxTokens * kMaxK];
+    uint32_t act[kMaxTokens];    // bit i: assignment i of the token is computed
+    uint32_t cnt[kMaxExperts];   // assignments per expert
+    uint32_t rec[kMaxExperts];   // experts recorded in the statistics this call
+    uint32_t off[kMaxExperts];   // first slot of each expert
+    uint32_t choff[kMaxExperts]; // first work item (chunk) of each expert
+    uint32_t rank[kMaxTokens * kMaxK];
+    uint32_t nchunks;
 };
 
-// math.topK (math.zig:130-174): heap seeded with the first k scores, later
-// scores replace the root only when strictly greater, results popped from the
-// root into positions k-1, k-2, ... (descending). Run by a whole wave for one
-// token: lane l holds scores l, l + 64, l + 128, l + 192 (n <= 256); the scan
-// reads score j with readlane, so the heap's values are uniform registers.
-__device__ float score_at(const float (&sc)[4], uint32_t j) {
-    const float v = j < 64 ? sc[0] : j < 128 ? sc[1] : j < 192 ? sc[2] : sc[3];
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)(j & 63)));
-}
-
-__device__ void top_k_wave(const float (&sc)[4], uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
-                           float (&ts)[kMaxK]) {
-    Heap4 h;
-    h.i0 = 0; h.s0 = score_at(sc, 0);
-    h.i1 = 1; h.s1 = k > 1 ? score_at(sc, 1) : 0.0f;
-    h.i2 = 2; h.s2 = k > 2 ? score_at(sc, 2) : 0.0f;
-    h.i3 = 3; h.s3 = k > 3 ? score_at(sc, 3) : 0.0f;
-    // for (i = k / 2; i > 0;) sift(--i, k)
-    if (k / 2 >= 2) h.sift1(k);
-    if (k / 2 >= 1) h.sift0(k);
-    for (uint32_t j = k; j < n; ++j) {
-        const float v = score_at(sc, j);
-        if (v > h.s0) {
-            h.i0 = j;
-            h.s0 = v;
-            h.sift0(k);
-        }
-    }
-    // Pop: result[ri] = root; root = heap[ri]; sift(0, ri), ri = k-1 .. 0.
-#pragma unroll
-    for (int ri = kMaxK - 1; ri >= 0; --ri) {
-        if ((uint32_t)ri >= k) continue;
-        ids[ri] = h.i0;
-        ts[ri] = h.s0;
-        if (ri == 3) { h.i0 = h.i3; h.s0 = h.s3; }
-        if (ri == 2) { h.i0 = h.i2; h.s0 = h.s2; }
-        if (ri == 1) { h.i0 = h.i1; h.s0 = h.s1; }
-        h.sift0((uint32_t)ri);
-    }
-}
-
-// The common case of topK without the heap: when the k + 1 largest scores
-// are distinct (and no score is NaN), the heap's result is exactly those k in
-// descending order. k + 1 rounds of a wave-wide max find them; a repeated
-// value in any round, or a NaN anywhere, returns false and the caller runs
-// the heap (ties and NaNs make the heap's insertion order matter).
-__device__ bool top_k_distinct(const float (&sc)[4], uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
-                               float (&ts)[kMaxK]) {
-    const uint32_t lane = threadIdx.x & 63;
-    uint32_t valid = 0;
-    bool nan = false;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        if (lane + 64 * q < n) {
-            valid |= 1u << q;
-            nan |= sc[q] != sc[q];
-        }
-    if (__any(nan)) return false;
-    const uint32_t rounds = k < n ? k + 1 : k;
-    for (uint32_t r = 0; r < rounds; ++r) {
-        float best = -__builtin_inff();
-        uint32_t best_q = 4, dup = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if (!((valid >> q) & 1u)) continue;
-            if (best_q == 4 || sc[q] > best) {
-                best = sc[q];
-                best_q = q;
-                dup = 0;
-            } else if (sc[q] == best) {
-                dup = 1;
-            }
-        }
-        float m = best_q < 4 ? best : -__builtin_inff();
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        const bool mine = best_q < 4 && best == m;
-        const unsigned long long who = __ballot(mine);
-        if (__popcll(who) != 1 || __any(mine && dup)) return false;
-        const uint32_t wl = (uint32_t)__builtin_ctzll(who);
-        const uint32_t wq = (uint32_t)__shfl((int)best_q, (int)wl, 64);
-        if (r < k) {
-            ids[r] = wl + 64 * wq;
-            ts[r] = m;
-        }
-        if (lane == wl) valid &= ~(1u << wq);
-    }
-    return true;
-}
-
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
-    __shared__ uint32_t s_ids[kMaxTokens * kMaxK];
-    __shared__ uint32_t s_act[kMaxTokens];  // bit i: assignment i of the token is computed
-    __shared__ uint32_t s_cnt[kMaxExperts];   // assignments per expert
-    __shared__ uint32_t s_off[kMaxExperts];   // first slot of each expert
-    __shared__ uint32_t s_choff[kMaxExperts]; // first work item (chunk) of each expert
-    __shared__ uint32_t s_rank[kMaxTokens * kMaxK];
-    __shared__ uint32_t s_nchunks;
+__device__ void route_body(const RouteArgs& a, RouteLds& L) {
+    uint32_t* const s_ids = L.ids;
+    uint32_t* const s_act = L.act;
+    uint32_t* const s_cnt = L.cnt;
+    uint32_t* const s_rec = L.rec;
+    uint32_t* const s_off = L.off;
+    uint32_t* const s_choff = L.choff;
+    uint32_t* const s_rank = L.rank;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6;
     const uint32_t T = a.n_tokens, E = a.n_experts, k = a.k;
-    for (uint32_t e = tid; e < E; e += kRouteThreads) s_cnt[e] = 0;
+    for (uint32_t e = tid; e < E; e += kRouteThreads) {
+        s_cnt[e] = 0;
+        s_rec[e] = 0;
+    }
+    __syncthreads();
 
     for (uint32_t t = wave; t < T; t += kRouteThreads / 64) {
-        const BufRsrc sr = make_rsrc(a.scores + (uint64_t)t * E, E * 4);
-        float sc[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sc[q] = __uint_as_float(buf_load_b32(sr, (lane + 64 * q) * 4, 0));
-        uint32_t ids[kMaxK] = {0, 0, 0, 0};
-        float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f}, w[kMaxK] = {0.f, 0.f, 0.f, 0.f};
-        if (!top_k_distinct(sc, E, k, ids, ts)) top_k_wave(sc, E, k, ids, ts);
-        // Softmax over the selected logits, then the routed scaling factor
-        // (scheduler.zig:184-201).
-        float mx = ts[0];
-        for (uint32_t i = 1; i < k; ++i)
-            if (ts[i] > mx) mx = ts[i];
-        float sum = 0.0f;
-        for (uint32_t i = 0; i < k; ++i) {
-            w[i] = expf(ts[i] - mx);
-            sum = sum + w[i];
-        }
-        for (uint32_t i = 0; i < k; ++i) w[i] = w[i] / sum;
-        for (uint32_t i = 0; i < k; ++i) w[i] = w[i] * a.scale;
-        // Heavy throttle keeps the top expert only and renormalises it
-        // (225-242); the others are deferred.
-        uint32_t act = (1u << k) - 1u, deferred = 0;
-        if (a.level == 3 && k > 1) {
-            act = 1u;
-            deferred = 1;
-            const float rem = 0.0f + w[0];
-            if (rem > 0.0f) w[0] = w[0] * (a.scale / rem);
-        }
+        const TokenRoute tr = route_token(a, t);
+        const uint32_t act = tr.act, deferred = tr.deferred;
+        const uint32_t(&ids)[kMaxK] = tr.ids;
+        const float(&w)[kMaxK] = tr.w;
         if (lane == 0) {
-            for (uint32_t i = 0; i < k; ++i) atomicAdd(a.counts + ids[i], 1ull);  // stats.record (220-222)
+            for (uint32_t i = 0; i < k; ++i) atomicAdd(&s_rec[ids[i]], 1u);  // stats.record (220-222)
             // RouteResult as moeFFN sees it (after the fallback).
             for (uint32_t i = 0; i < kMaxK; ++i) {
                 if (a.route_ids) a.route_ids[t * kMaxK + i] = i < k ? ids[i] : 0xFFFFFFFFu;
@@ -214,6 +75,9 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         }
     }
     __syncthreads();
+    // Statistics: one device atomic per recorded expert.
+    for (uint32_t e = tid; e < E; e += kRouteThreads)
+        if (s_rec[e]) atomicAdd(a.counts + e, (unsigned long long)s_rec[e]);
 
     if (T == 1) {
         // Decode: slots in route order; GEMV problem lists.
@@ -273,7 +137,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
             carry += (uint32_t)__shfl((int)inc, 63, 64);
             carry_ch += (uint32_t)__shfl((int)inc_ch, 63, 64);
         }
-        if (lane == 0) s_nchunks = carry_ch;
+        if (lane == 0) L.nchunks = carry_ch;
     }
     __syncthreads();
     for (uint32_t p = tid; p < T * kMaxK; p += kRouteThreads) {
@@ -295,7 +159,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
             a.work_dn[q] = QmmWork{e, off + c0, m, 0};
         }
     }
-    const uint32_t nch = s_nchunks;
+    const uint32_t nch = L.nchunks;
     const bool sh = a.shared && a.shared_merged;
     const uint32_t sh_chunks = sh ? (T + kQmmTokens - 1) / kQmmTokens : 0;
     for (uint32_t c = tid; c < sh_chunks; c += kRouteThreads) {
@@ -309,6 +173,12 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
         a.n_work[1] = nch + sh_chunks;
     }
 }
+
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
+    __shared__ RouteLds L;
+    route_body(a, L);
+}
+
 
 __global__ void combine_kernel(const float* __restrict__ eo, const int32_t* __restrict__ assign_slot,
                                const float* __restrict__ assign_w, const int32_t* __restrict__ shared_slot,

@@ -1,0 +1,204 @@
+// Routing of one token (Scheduler.route, scheduler.zig:169-262), run by a
+// whole wave: math.topK over the router scores, softmax over the selected
+// logits, the routed scaling factor and the heavy-throttle top-1 fallback.
+// Shared by the routing kernel and the decode gate/up GEMV, which routes
+// its single token itself (every wave computes the same result).
+#pragma once
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace mmhip {
+
+constexpr int kMaxK = 4;
+
+// The size-k min-heap of math.topK (math.zig:130-193) for k <= 4, held in
+// registers: every position is a compile-time index, so siftDownMin's
+// comparisons (children 2p+1, 2p+2 of parent p, strict <, left first) are
+// spelled out for the only parents a heap of <= 4 entries has: 0 and 1.
+struct Heap4 {
+    uint32_t i0, i1, i2, i3;
+    float s0, s1, s2, s3;
+    __device__ void swap01() {
+        uint32_t ti = i0; i0 = i1; i1 = ti;
+        float ts = s0; s0 = s1; s1 = ts;
+    }
+    __device__ void swap02() {
+        uint32_t ti = i0; i0 = i2; i2 = ti;
+        float ts = s0; s0 = s2; s2 = ts;
+    }
+    __device__ void swap13() {
+        uint32_t ti = i1; i1 = i3; i3 = ti;
+        float ts = s1; s1 = s3; s3 = ts;
+    }
+    // siftDownMin(start = 1, end): the only child of position 1 is 3.
+    __device__ void sift1(uint32_t end) {
+        if (3 < end && s3 < s1) swap13();
+    }
+    // siftDownMin(start = 0, end).
+    __device__ void sift0(uint32_t end) {
+        uint32_t smallest = 0;
+        float sm = s0;
+        if (1 < end && s1 < sm) {
+            smallest = 1;
+            sm = s1;
+        }
+        if (2 < end && s2 < sm) smallest = 2;
+        if (smallest == 1) {
+            swap01();
+            sift1(end);
+        } else if (smallest == 2) {
+            swap02();  // position 2 has no children below 4
+        }
+    }
+};
+
+// math.topK (math.zig:130-174): heap seeded with the first k scores, later
+// scores replace the root only when strictly greater, results popped from the
+// root into positions k-1, k-2, ... (descending). Run by a whole wave for one
+// token: lane l holds scores l, l + 64, l + 128, l + 192 (n <= 256); the scan
+// reads score j with readlane, so the heap's values are uniform registers.
+__device__ __forceinline__ float score_at(const float (&sc)[4], uint32_t j) {
+    // Uniform branches, one readlane each: a select over the four registers
+    // would be lowered to an indexed scratch access.
+    const int l = (int)(j & 63u);
+    const uint32_t q = j >> 6;
+    if (q == 0) return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc[0]), l));
+    if (q == 1) return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc[1]), l));
+    if (q == 2) return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc[2]), l));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc[3]), l));
+}
+
+__device__ inline void top_k_wave(const float (&sc)[4], uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
+                           float (&ts)[kMaxK]) {
+    Heap4 h;
+    h.i0 = 0; h.s0 = score_at(sc, 0);
+    h.i1 = 1; h.s1 = k > 1 ? score_at(sc, 1) : 0.0f;
+    h.i2 = 2; h.s2 = k > 2 ? score_at(sc, 2) : 0.0f;
+    h.i3 = 3; h.s3 = k > 3 ? score_at(sc, 3) : 0.0f;
+    // for (i = k / 2; i > 0;) sift(--i, k)
+    if (k / 2 >= 2) h.sift1(k);
+    if (k / 2 >= 1) h.sift0(k);
+    for (uint32_t j = k; j < n; ++j) {
+        const float v = score_at(sc, j);
+        if (v > h.s0) {
+            h.i0 = j;
+            h.s0 = v;
+            h.sift0(k);
+        }
+    }
+    // Pop: result[ri] = root; root = heap[ri]; sift(0, ri), ri = k-1 .. 0.
+#pragma unroll
+    for (int ri = kMaxK - 1; ri >= 0; --ri) {
+        if ((uint32_t)ri >= k) continue;
+        ids[ri] = h.i0;
+        ts[ri] = h.s0;
+        if (ri == 3) { h.i0 = h.i3; h.s0 = h.s3; }
+        if (ri == 2) { h.i0 = h.i2; h.s0 = h.s2; }
+        if (ri == 1) { h.i0 = h.i1; h.s0 = h.s1; }
+        h.sift0((uint32_t)ri);
+    }
+}
+
+// The common case of topK without the heap: when the k + 1 largest scores
+// are distinct (and no score is NaN), the heap's result is exactly those k in
+// descending order. k + 1 rounds of a wave-wide max find them; a repeated
+// value in any round, or a NaN anywhere, returns false and the caller runs
+// the heap (ties and NaNs make the heap's insertion order matter).
+__device__ inline bool top_k_distinct(const float (&sc)[4], uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
+                               float (&ts)[kMaxK]) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t valid = 0;
+    bool nan = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (lane + 64 * q < n) {
+            valid |= 1u << q;
+            nan |= sc[q] != sc[q];
+        }
+    if (__any(nan)) return false;
+    const uint32_t rounds = k < n ? k + 1 : k;
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxK + 1; ++r) {  // constant r: ids / ts stay in registers
+        if (r >= rounds) break;
+        float best = -__builtin_inff();
+        uint32_t best_q = 4, dup = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (!((valid >> q) & 1u)) continue;
+            if (best_q == 4 || sc[q] > best) {
+                best = sc[q];
+                best_q = q;
+                dup = 0;
+            } else if (sc[q] == best) {
+                dup = 1;
+            }
+        }
+        float m = best_q < 4 ? best : -__builtin_inff();
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        const bool mine = best_q < 4 && best == m;
+        const unsigned long long who = __ballot(mine);
+        if (__popcll(who) != 1 || __any(mine && dup)) return false;
+        const uint32_t wl = (uint32_t)__builtin_ctzll(who);
+        const uint32_t wq = (uint32_t)__shfl((int)best_q, (int)wl, 64);
+        if (r < k) {
+            ids[r] = wl + 64 * wq;
+            ts[r] = m;
+        }
+        if (lane == wl) valid &= ~(1u << wq);
+    }
+    return true;
+}
+
+// The routing of token t (uniform across the wave). ids / w hold the k
+// selected experts in topK order and their weights after the fallback; bit i
+// of act is set when assignment i is computed; deferred is the fallback flag.
+struct TokenRoute {
+    uint32_t ids[kMaxK];
+    float w[kMaxK];
+    uint32_t act, deferred;
+};
+__device__ inline TokenRoute route_token(const RouteArgs& a, uint32_t t) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t E = a.n_experts, k = a.k;
+    const BufRsrc sr = make_rsrc(a.scores + (uint64_t)t * E, E * 4);
+    float sc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sc[q] = __uint_as_float(buf_load_b32(sr, (lane + 64 * q) * 4, 0));
+    TokenRoute r{{0, 0, 0, 0}, {0.f, 0.f, 0.f, 0.f}, 0, 0};
+    float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f};
+    if (!top_k_distinct(sc, E, k, r.ids, ts)) top_k_wave(sc, E, k, r.ids, ts);
+    // Softmax over the selected logits, then the routed scaling factor
+    // (scheduler.zig:184-201). Loops run over kMaxK with a k test so that
+    // every array index is a compile-time constant (registers, no scratch).
+    float mx = ts[0];
+#pragma unroll
+    for (uint32_t i = 1; i < kMaxK; ++i)
+        if (i < k && ts[i] > mx) mx = ts[i];
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i)
+        if (i < k) {
+            r.w[i] = expf(ts[i] - mx);
+            sum = sum + r.w[i];
+        }
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i)
+        if (i < k) r.w[i] = r.w[i] / sum;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i)
+        if (i < k) r.w[i] = r.w[i] * a.scale;
+    // Heavy throttle keeps the top expert only and renormalises it
+    // (225-242); the others are deferred.
+    r.act = (1u << k) - 1u;
+    if (a.level == 3 && k > 1) {
+        r.act = 1u;
+        r.deferred = 1;
+        const float rem = 0.0f + r.w[0];
+        if (rem > 0.0f) r.w[0] = r.w[0] * (a.scale / rem);
+    }
+    return r;
+}
+
+}  // namespace mmhip

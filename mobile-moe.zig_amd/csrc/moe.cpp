@@ -4,11 +4,13 @@
 //
 // One call enqueues, on the context stream:
 //   router scores   f32/f16 GEMV, [T][E]                     "moe_router"
-//   route           heap top-k, softmax, throttle, counts,
+//   T > 1: route    heap top-k, softmax, throttle, counts,
 //                   slot layout and problem lists            "moe_route"
 //   T == 1 (decode):
 //     gate/up       quantised GEMV over the routed (+ shared)
-//                   experts' gate and up matrices            "moe_gateup"
+//                   experts' gate and up matrices; every
+//                   workgroup routes the token itself and one
+//                   writes the routing outputs               "moe_gateup"
 //     down          quantised GEMV, input silu(gate) * up
 //                   formed while quantising                  "moe_down"
 //   T > 1 (prefill, experts grouped):
@@ -140,7 +142,7 @@ size_t carve(mmhip_moe_layer* L, char* base) {
 
 int gemv_launch(mmhip_ctx* ctx, const mmhip_weight* w, const char* family, const uint4* probs, const uint32_t* n_active,
                 uint32_t n_probs, const float* x, uint64_t x_stride, uint64_t x2_off, bool silu, float* y,
-                uint64_t y_stride) {
+                uint64_t y_stride, const RouteArgs* route = nullptr) {
     const TileGeom& g = w->geom;
     GemvArgs a{};
     a.recs = w->recs;
@@ -162,6 +164,10 @@ int gemv_launch(mmhip_ctx* ctx, const mmhip_weight* w, const char* family, const
     a.units = (uint32_t)g.units;
     a.rows = (uint32_t)g.rows;
     a.cols = (uint32_t)g.cols;
+    if (route) {
+        a.route = *route;
+        a.route_decode = 1;
+    }
     hipError_t e;
     {
         TimedLaunch tl(ctx, family);
@@ -183,11 +189,6 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
                 bool with_bias, uint32_t* route_ids, float* route_w) {
     const uint32_t H = L->hidden, I = L->inter, E = L->n_experts;
     hipStream_t s = ctx->stream;
-    {
-        TimedLaunch tl(ctx, "moe_router");
-        MOE_TRY(check_hip(launch_gemv_float(L->router->plain, L->router_type, 0, hidden, H, L->scores, E, T, E, H, s),
-                          "moe: router"));
-    }
     RouteArgs r{};
     r.scores = L->scores;
     r.n_tokens = T;
@@ -213,13 +214,20 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
     r.n_work = L->n_work;
     r.inter = I;
     {
+        TimedLaunch tl(ctx, "moe_router");
+        MOE_TRY(check_hip(launch_gemv_float(L->router->plain, L->router_type, 0, hidden, H, L->scores, E, T, E, H, s),
+                          "moe: router"));
+    }
+    if (T > 1) {
         TimedLaunch tl(ctx, "moe_route");
         MOE_TRY(check_hip(launch_route(r, s), "moe: route"));
     }
     const bool sep_shared = L->has_shared && !L->shared_merged;
     const uint32_t SI = L->shared_inter;
     if (T == 1) {
-        MOE_TRY(gemv_launch(ctx, L->gu, "moe_gateup", L->gemv_gu, L->n_gemv, 10, hidden, 0, 0, false, L->y_gu, I));
+        // Decode: the gate/up GEMV routes the token itself (no routing launch).
+        MOE_TRY(gemv_launch(ctx, L->gu, "moe_gateup", nullptr, nullptr, L->shared_merged ? 10 : 8, hidden, 0, 0, false,
+                            L->y_gu, I, &r));
         if (sep_shared)
             MOE_TRY(gemv_launch(ctx, L->sh_gu, "moe_gateup", nullptr, nullptr, 2, hidden, 0, 0, false, L->y_sh, SI));
         MOE_TRY(gemv_launch(ctx, L->dn, "moe_down", L->gemv_dn, L->n_gemv + 1, 5, L->y_gu, 2 * (uint64_t)I, I, true,
