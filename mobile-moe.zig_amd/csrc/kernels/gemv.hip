@@ -86,14 +86,15 @@ struct StepPos {
 //
 // Loads: every weight, scale and activation load goes through a buffer
 // resource and is issued unconditionally (out-of-range offsets for steps past
-// the wave's end), so each wait covers exactly the loads it needs. The
-// prologue issues the table and activation loads, waits for them, fills LDS,
-// and only then starts the weight stream: a CU returns loads in issue order
-// across its waves, and a wave cannot issue while the CU's load queue is
-// full, so weights issued first would delay every wave's prologue. The
-// stream runs one step ahead (two register buffers): the CU's queue holds
-// about one step per wave, and a deeper prefetch only blocks the issuing
-// wave.
+// the wave's end), so each wait covers exactly the loads it needs. A CU
+// returns loads in issue order across its waves, and a wave cannot issue
+// while the CU's load queue is full: weights issued before another wave's
+// prologue loads would delay that wave's prologue. So every wave issues its
+// table and activation loads, a barrier orders the issue, and only then do
+// the first weight steps go out; the waits for the prologue data leave them
+// in flight while LDS is filled. The stream runs one step ahead (two register
+// buffers): the CU's queue holds about one step per wave, and a deeper
+// prefetch only blocks the issuing wave.
 template <int FMT, int UPS, int WG, int DEPTH, bool ROUTE>
 __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     constexpr uint32_t kWaves = WG / 64;
@@ -228,13 +229,15 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
         float xv[4], uv[4];
         x_pass_load(x_r, 0, xv);
         x_pass_load(u_r, 0, uv);
-        vm_wait_all();
-        // When one pass covers the chunk, no activation load follows, and the
-        // first weight steps go out now so that their latency overlaps the LDS
-        // fill below (a later activation load would wait behind them).
+        // The first weight steps go out now, behind every wave's table and
+        // activation loads (the barrier orders the issue; the CU returns
+        // loads in issue order), so their HBM latency overlaps the prologue's
+        // loads and the LDS fill below; the waits for the prologue data leave
+        // them in flight. Activation passes beyond the first (chunks wider
+        // than WG / 8 blocks) return behind them.
         start_chunk(nb);
-        const bool early = nb <= WG / 8;
-        if (early) issue_first();
+        __builtin_amdgcn_s_barrier();
+        issue_first();
         if (FMT == kFmtIq2) tc.store(tab);
         for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) row_sum[i] = 0.0f;
         if (silu_mul) silu_mul4(xv, uv);
@@ -246,7 +249,6 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
             if (silu_mul) silu_mul4(v, u);
             x_pass_store(v, nb, b0, aq, xs);
         }
-        if (!early) issue_first();
     }
     uint32_t kb = 0;
     for (;;) {
