@@ -26,45 +26,6 @@ namespace {
 constexpr uint32_t kChunkBlocks = 256;  // 8192 columns of activation per LDS chunk (multiple of 8)
 constexpr uint32_t kGemvMaxTiles = 64;  // tiles per workgroup (LDS row sums)
 
-// The routing outputs of a decode call (the single-token branch of the
-// routing kernel): route ids / weights, statistics, slots in route order,
-// the shared slot, and the down problem list. One thread.
-__device__ __forceinline__ void decode_route_outputs(const RouteArgs& a, const TokenRoute& tr) {
-    const uint32_t E = a.n_experts, k = a.k;
-#pragma unroll
-    for (uint32_t i = 0; i < kMaxK; ++i) {
-        if (a.route_ids) a.route_ids[i] = i < k ? tr.ids[i] : 0xFFFFFFFFu;
-        if (a.route_w) a.route_w[i] = i < k ? tr.w[i] : 0.0f;
-        a.assign_w[i] = ((tr.act >> i) & 1u) ? tr.w[i] : 0.0f;
-        a.assign_slot[i] = -1;
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < kMaxK; ++i)
-        if (i < k) atomicAdd(a.counts + tr.ids[i], 1ull);  // stats.record
-    a.deferred[0] = tr.deferred;
-    a.shared_slot[0] = a.shared ? 4 : -1;
-    a.slot_tok[4] = 0;
-    uint32_t s = 0;
-#pragma unroll
-    for (uint32_t i = 0; i < kMaxK; ++i) {
-        if (i >= k || !((tr.act >> i) & 1u)) continue;
-        a.assign_slot[i] = (int32_t)s;
-        a.slot_tok[s] = 0;
-        a.gemv_gu[2 * s] = make_uint4(tr.ids[i], 0, 2 * s, 0);
-        a.gemv_gu[2 * s + 1] = make_uint4(E + tr.ids[i], 0, 2 * s + 1, 0);
-        a.gemv_dn[s] = make_uint4(tr.ids[i], s, s, 0);
-        ++s;
-    }
-    uint32_t n_gu = 2 * s, n_dn = s;
-    if (a.shared && a.shared_merged) {
-        a.gemv_gu[n_gu++] = make_uint4(2 * E, 0, 8, 0);
-        a.gemv_gu[n_gu++] = make_uint4(2 * E + 1, 0, 9, 0);
-        a.gemv_dn[n_dn++] = make_uint4(E, 4, 4, 0);
-    }
-    a.n_gemv[0] = n_gu;
-    a.n_gemv[1] = n_dn;
-}
-
 // Position of a decode step: tile t (within the workgroup's range) and step s
 // within the tile's part of the current K-chunk.
 struct StepPos {
@@ -418,6 +379,8 @@ static const void* kernel_for_wg(int wg, int ups) {
 
 hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStream_t s) {
     if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
+    static const bool iq2_old = getenv("MMHIP_IQ2_OLD") != nullptr;
+    if (fmt == kFmtIq2 && !iq2_old) return launch_gemv_iq2(a_in, num_cu, s);
     GemvArgs a = a_in;
     // Per-format defaults, measured on MI355X with 64-expert batches:
     //   IQ2_XXS (decode-bound): 1024 threads, one workgroup per CU (16 waves

@@ -1,0 +1,420 @@
+// IQ2_XXS decode GEMV on gfx950 (matVecMulUnified's non-Q8_0 branch,
+// inference.zig:1222-1226, and the expert products of expertFFN,
+// inference.zig:1171-1185, without the f32 dequantization round trip).
+//
+// One 1024-thread workgroup per CU owns one problem (matrix + activation
+// vector) and up to kQMaxTiles 16-row tiles. The activation is quantised into
+// LDS per K-chunk of up to 8 record units (2048 columns) as two int8 digit
+// planes per 32-column block (x ~ s (256 hi + lo)).
+//
+// Work items are (unit, tile) pairs in unit-major order, taken two tiles at a
+// time (tiles 2tp and 2tp + 1 of one unit) and split into 16 equal
+// contiguous runs of such pairs, one per wave, so a wave keeps one unit's
+// activation operands in registers while it walks tiles, and the two items
+// of a pair give it two independent MFMA chains. The A operands are sparse: for
+// the MFMA of block s (s = 0..7 within the unit) only the lanes whose A row
+// m = 4j + e belongs to block s hold digits (e = 0/1: hi/lo digits of block j,
+// e = 2/3: of block j + 4), all others hold zero. The eight MFMAs of a unit
+// accumulate into one result, whose D rows 4g..4g+3 in lane (g, n) are then
+// the hi/lo dot products of blocks g and g + 4 of row n: no cross-lane
+// gather, two digit combines per item, and lane (g, n) scales exactly the two
+// sub-blocks whose ls bits its own record dwords carry.
+//
+// B operands come from LDS tables (record layout in device_common.hpp): the
+// 8-byte table keyed by b012 | P | idx, whose high dword still needs the hi3
+// signs (iq2_fix_hi), or, for the first kTwo even sub-block slots, the low
+// dword from that table and the fully signed high dword from a second 16 KiB
+// table keyed by P | idx | hi3 (record bits 6..17). The two paths trade VALU
+// (sign fix) against LDS bandwidth (a second random read). The table reads
+// of both items of a pair are issued before either is used.
+//
+// Each item leaves its 64 lane partial sums in LDS; after a chunk, every
+// output row adds its (unit, lane group) partials in a fixed order, so the
+// result does not depend on timing.
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "route_ops.hpp"
+
+namespace mmhip {
+
+namespace {
+
+constexpr int kQWg = 1024;
+constexpr uint32_t kQWaves = kQWg / 64;
+constexpr uint32_t kQChunkUnits = 8;                 // record units per activation chunk
+constexpr uint32_t kQChunkBlocks = kQChunkUnits * 8;  // 32-column blocks per chunk
+constexpr uint32_t kQMaxTiles = 32;                  // row tiles per workgroup
+
+// Second table: entry (P | idx << 1 | hi3 << 9) = columns 4..7 of grid entry
+// idx with signs hi3 (columns 4..6) and P ^ parity(hi3) (column 7, the
+// ksigns parity bit).
+struct Iq2HiTable {
+    uint32_t w[4096];
+};
+constexpr Iq2HiTable make_iq2_hi_table() {
+    Iq2HiTable t{};
+    for (uint32_t e = 0; e < 4096; ++e) {
+        const uint32_t par = e & 1u, idx = (e >> 1) & 0xFFu, hi3 = e >> 9;
+        t.w[e] = negate_bytes((uint32_t)(kIq2Grid[idx] >> 32), nibble_byte_mask(hi3 | ((par ^ parity3(hi3)) << 3)));
+    }
+    return t;
+}
+static __constant__ Iq2HiTable c_iq2_hi = make_iq2_hi_table();
+
+// Quantises 4 columns per lane (8 lanes per 32-column block, quantize_quad)
+// into the chunk's digit planes: aq[(b * 2 + digit) * 32 + column].
+__device__ __forceinline__ void x_store_planes(const float (&v)[4], uint32_t nblk, uint32_t b0, uint8_t* aq,
+                                               float* xs) {
+    uint32_t h4, l4;
+    const float s = quantize_quad(v, h4, l4);
+    const uint32_t b = b0 + (threadIdx.x >> 3), jq = threadIdx.x & 7;
+    if (b < nblk) {
+        *reinterpret_cast<uint32_t*>(aq + b * 64 + 4 * jq) = h4;
+        *reinterpret_cast<uint32_t*>(aq + b * 64 + 32 + 4 * jq) = l4;
+        if (jq == 0) xs[b] = s;
+    }
+}
+
+// Activation columns [c0, c0 + 32 nblk) of the problem's vector (times
+// silu(x) * u when silu_mul) into the digit planes; 128 blocks per pass.
+__device__ __forceinline__ void quantize_planes(BufRsrc xr, BufRsrc ur, bool silu_mul, uint32_t nblk, uint8_t* aq,
+                                                float* xs) {
+    for (uint32_t b0 = 0; b0 < nblk; b0 += kQWg / 8) {
+        float v[4], u[4];
+        x_pass_load(xr, b0, v);
+        x_pass_load(ur, b0, u);
+        if (silu_mul) silu_mul4(v, u);
+        x_store_planes(v, nblk, b0, aq, xs);
+    }
+}
+
+// Problem p of the launch: matrix, activation row and output row; false when
+// the problem does not run in this call.
+template <bool ROUTE>
+__device__ __forceinline__ bool select_problem(const GemvArgs& a, uint32_t p, uint64_t& mat, uint64_t& x_row,
+                                               uint64_t& y_row) {
+    mat = a.first_mat + p;
+    x_row = p;
+    y_row = p;
+    if constexpr (ROUTE) {
+        // Every wave routes the token (same result); the problem follows.
+        const TokenRoute tr = route_token(a.route, 0);
+        if (p == 0 && blockIdx.x == 0 && threadIdx.x == 0) decode_route_outputs(a.route, tr);
+        const uint32_t E = a.route.n_experts;
+        uint32_t n_act = 0, e_sel = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < kMaxK; ++i)
+            if (i < a.route.k && ((tr.act >> i) & 1u)) {
+                if (n_act == p >> 1) e_sel = tr.ids[i];
+                ++n_act;
+            }
+        x_row = 0;
+        if (p < 2 * n_act) {
+            mat = (p & 1u) ? E + e_sel : e_sel;
+            return true;
+        }
+        if (a.route.shared && a.route.shared_merged && p < 2 * n_act + 2) {
+            mat = 2 * E + (p - 2 * n_act);
+            y_row = 8 + (p - 2 * n_act);
+            return true;
+        }
+        return false;
+    } else {
+        if (a.n_active && p >= *a.n_active) return false;
+        if (a.probs) {
+            const uint4 d = a.probs[p];
+            mat = d.x;
+            x_row = d.y;
+            y_row = d.z;
+        }
+        return true;
+    }
+}
+
+// Position of an item: unit ul within the chunk, tile t within the
+// workgroup's range (unit-major order).
+struct ItemPos {
+    uint32_t ul, t;
+};
+
+// Raw table words of one record unit (lane's 8 records): .x = low dword,
+// .y = high dword (final for two-table slots, hi3 signs still to apply for
+// the others).
+struct RawB {
+    uint2 e[8];
+};
+
+template <int TWO>
+__device__ __forceinline__ void fetch_b(const uint4& r, const uint32_t* tab, const uint32_t* hitab, RawB& raw) {
+    const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+    const char* t8 = reinterpret_cast<const char*>(tab);
+    const char* th = reinterpret_cast<const char*>(hitab);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const uint32_t d = w4[s >> 1];
+        if ((s & 1) == 0 && (s >> 1) < TWO) {
+            raw.e[s].x = *reinterpret_cast<const uint32_t*>(t8 + (d & 0x7FF8u));
+            raw.e[s].y = *reinterpret_cast<const uint32_t*>(th + ((d >> 4) & 0x3FFCu));
+        } else {
+            const uint32_t addr = (s & 1) ? ((d >> 15) & 0x7FF8u) : (d & 0x7FF8u);
+            raw.e[s] = *reinterpret_cast<const uint2*>(t8 + addr);
+        }
+    }
+}
+
+template <int TWO>
+__device__ __forceinline__ void finish_b(const uint4& r, const RawB& raw, long (&b)[8]) {
+    const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const uint32_t d = w4[s >> 1];
+        uint32_t hi = raw.e[s].y;
+        if (!((s & 1) == 0 && (s >> 1) < TWO)) hi = iq2_fix_hi(hi, (s & 1) ? (d & 7u) : ((d >> 15) & 7u));
+        b[s] = (long)(((uint64_t)hi << 32) | (uint64_t)raw.e[s].x);
+    }
+}
+
+template <int TWO, int DEPTH, bool ROUTE>
+__global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
+    constexpr int kRing = DEPTH + 1;
+    // One LDS block with the tables first: their byte offsets (below 48 KiB)
+    // fold into the ds_read offset fields.
+    struct Lds {
+        uint32_t tab[kIq2TableWords];
+        uint32_t hitab[TWO > 0 ? 4096 : 4];
+        float part[kQChunkUnits * kQMaxTiles * 64];
+        uint8_t aq[kQChunkBlocks * 64];
+        float xs[kQChunkBlocks];
+        float row_sum[kQMaxTiles * 16];
+    };
+    __shared__ __align__(16) Lds lds;
+    uint32_t* const tab = lds.tab;
+    uint32_t* const hitab = lds.hitab;
+    float* const part = lds.part;
+    uint8_t* const aq = lds.aq;
+    float* const xs = lds.xs;
+    float* const row_sum = lds.row_sum;
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t n = lane & 15, g = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint64_t mat, x_row, y_row;
+    if (!select_problem<ROUTE>(a, blockIdx.y, mat, x_row, y_row)) return;  // whole workgroup
+    const float* x = a.x + x_row * a.x_stride;
+    float* const y_base = a.y + y_row * a.y_stride;
+    const bool silu_mul = a.silu_mul != 0;
+    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;  // < a.tiles (grid size)
+    const uint32_t n_tiles = min(a.tiles - t_begin, a.tiles_per_wg);
+    const BufRsrc rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
+    const BufRsrc d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
+    const uint32_t rec_voff = lane * 16;
+    const uint32_t d_voff = n * a.d_row * 2;
+    // Sparse A row of this lane: block s_star of the unit, digit d_star.
+    const uint32_t s_star = (n >> 2) + 4 * ((n >> 1) & 1u), d_star = n & 1u;
+
+    // Per-chunk state (set by start_chunk). Items are processed in pairs
+    // (tiles 2tp and 2tp + 1 of one unit, the second absent when the tile
+    // count is odd), so a pair never spans two units.
+    uint32_t u0 = 0, uc = 1, tp_n = 1, p0 = 0, p1 = 0;
+    auto start_chunk = [&](uint32_t chunk_u0, uint32_t units_in_chunk) {
+        u0 = chunk_u0;
+        uc = units_in_chunk;
+        tp_n = (n_tiles + 1) / 2;
+        const uint32_t N = uc * tp_n;
+        p0 = wave * N / kQWaves;
+        p1 = (wave + 1) * N / kQWaves;
+    };
+    auto advance = [&](ItemPos q) { return (q.t + 1 == tp_n) ? ItemPos{q.ul + 1, 0} : ItemPos{q.ul, q.t + 1}; };
+    // Loads both items of pair q (ItemPos.t = pair index within the unit).
+    auto load = [&](bool valid, ItemPos q, uint4 (&r)[2], uint32_t (&dbits)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t rs = kBufOob, ds = kBufOob;
+            const uint32_t tl = 2 * q.t + h;
+            if (valid && tl < n_tiles) {
+                const uint32_t tile = t_begin + tl, u = u0 + q.ul;
+                rs = (tile * a.units + u) * 1024;
+                ds = (tile * 16 * a.d_row + u) * 2;
+            }
+            r[h] = buf_load_b128<kCacheStream>(rec_r, rec_voff, rs);
+            dbits[h] = buf_load_b16<kCacheStream>(d_r, d_voff, ds);
+        }
+    };
+
+    uint4 rb[kRing][2];
+    uint32_t db[kRing][2];
+    ItemPos cur{0, 0}, nxt{0, 0};
+    auto issue_first = [&]() {
+        cur = ItemPos{p0 / tp_n, p0 % tp_n};
+        nxt = cur;
+#pragma unroll
+        for (int q = 0; q < DEPTH; ++q) {
+            load(p0 + q < p1, nxt, rb[q], db[q]);
+            nxt = advance(nxt);
+        }
+    };
+
+    {
+        // Prologue: tables and the first activation chunk load, every wave's
+        // loads issued (barrier) before any weight load, then the first
+        // weight items go out while LDS is filled.
+        const uint32_t uc0 = min(a.units, kQChunkUnits);
+        const uint32_t nb = uc0 * 8;
+        const uint32_t xb = min(a.cols, nb * 32) * 4;
+        const BufRsrc x_r = make_rsrc(x, xb);
+        const BufRsrc u_r = make_rsrc(x + a.x2_off, silu_mul ? xb : 0);  // zero-size: loads read 0
+        const BufRsrc t_r = make_rsrc(&c_iq2_tables, sizeof(Iq2Tables));
+        const BufRsrc h_r = make_rsrc(&c_iq2_hi, sizeof(Iq2HiTable));
+        uint4 tv[2], hv;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) tv[i] = buf_load_b128(t_r, (threadIdx.x + kQWg * i) * 16, 0);
+        if (TWO > 0) hv = buf_load_b128(h_r, threadIdx.x * 16, 0);
+        float xv[4], uv[4];
+        x_pass_load(x_r, 0, xv);
+        x_pass_load(u_r, 0, uv);
+        start_chunk(0, uc0);
+        __builtin_amdgcn_s_barrier();
+        issue_first();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) reinterpret_cast<uint4*>(tab)[threadIdx.x + kQWg * i] = tv[i];
+        if (TWO > 0) reinterpret_cast<uint4*>(hitab)[threadIdx.x] = hv;
+        for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += kQWg) row_sum[i] = 0.0f;
+        if (silu_mul) silu_mul4(xv, uv);
+        x_store_planes(xv, nb, 0, aq, xs);  // one pass covers 128 >= 64 blocks
+    }
+
+    for (uint32_t kc = 0;;) {
+        lds_barrier();  // tables, digit planes, scales (and row sums) visible
+        long av[8];
+        float xa = 0.0f, xb = 0.0f, ha = 0.0f, hb = 0.0f;
+        uint32_t a_ul = 0xFFFFFFFFu;
+        for (uint32_t i = p0; i < p1; i += kRing) {
+#pragma unroll
+            for (int q = 0; q < kRing; ++q) {
+                if (i + q < p1) {
+                    load(i + q + DEPTH < p1, nxt, rb[(q + DEPTH) % kRing], db[(q + DEPTH) % kRing]);
+                    nxt = advance(nxt);
+                    if (cur.ul != a_ul) {
+                        // This unit's sparse A operands and block scales.
+                        a_ul = cur.ul;
+                        const uint8_t* ap = aq + ((a_ul * 8 + s_star) * 2 + d_star) * 32 + 8 * g;
+                        const uint2 xw = *reinterpret_cast<const uint2*>(ap);
+                        const long xl = (long)(((uint64_t)xw.y << 32) | (uint64_t)xw.x);
+#pragma unroll
+                        for (int s = 0; s < 8; ++s) av[s] = ((uint32_t)s == s_star) ? xl : 0;
+                        xa = xs[a_ul * 8 + g] * 0.25f;
+                        xb = xs[a_ul * 8 + g + 4] * 0.25f;
+                        ha = xa * 0.5f;
+                        hb = xb * 0.5f;
+                    }
+                    // B operands of both items: all table reads first.
+                    RawB raw0, raw1;
+                    fetch_b<TWO>(rb[q][0], tab, hitab, raw0);
+                    fetch_b<TWO>(rb[q][1], tab, hitab, raw1);
+                    long b0[8], b1[8];
+                    finish_b<TWO>(rb[q][0], raw0, b0);
+                    finish_b<TWO>(rb[q][1], raw1, b1);
+                    v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+#pragma unroll
+                    for (int s = 0; s < 8; ++s) {
+                        acc0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[s], b0[s], acc0, 0, 0, 0);
+                        acc1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[s], b1[s], acc1, 0, 0, 0);
+                    }
+                    // Blocks g and g + 4 of row n: d * (0.5 + ls) / 4 * s_x * digits.
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const v4i& acc = h ? acc1 : acc0;
+                        const uint4& r = rb[q][h];
+                        const float df = f16_scale(db[q][h]);
+                        const float sa = fmaf((float)iq2_ls_a(r), xa, ha);
+                        const float sb = fmaf((float)iq2_ls_b(r), xb, hb);
+                        float v = (float)digits_combine(acc[0], acc[1]) * sa;
+                        v = fmaf((float)digits_combine(acc[2], acc[3]), sb, v);
+                        const uint32_t tl = 2 * cur.t + h;
+                        if (tl < n_tiles) part[(cur.ul * n_tiles + tl) * 64 + lane] = v * df;
+                    }
+                    cur = advance(cur);
+                }
+            }
+        }
+        lds_barrier();  // every item's partials written
+        // Row sums: units in order, lane groups in order.
+        for (uint32_t idx = threadIdx.x; idx < n_tiles * 16; idx += kQWg) {
+            const uint32_t t = idx >> 4, rr = idx & 15;
+            float sum = 0.0f;
+            for (uint32_t ul = 0; ul < uc; ++ul) {
+                const float* pp = part + (ul * n_tiles + t) * 64 + rr;
+                sum += ((pp[0] + pp[16]) + pp[32]) + pp[48];
+            }
+            row_sum[idx] += sum;
+        }
+        kc += uc;
+        if (kc >= a.units) break;
+        // Next K-chunk: re-quantise the activation (the planes and partials
+        // are free once every wave passed the barrier below).
+        lds_barrier();
+        const uint32_t ucn = min(a.units - kc, kQChunkUnits);
+        const uint32_t c0 = kc * 256;
+        const uint32_t cb = (a.cols > c0 ? min(a.cols - c0, ucn * 256) : 0) * 4;
+        quantize_planes(make_rsrc(x + c0, cb), make_rsrc(x + a.x2_off + c0, silu_mul ? cb : 0), silu_mul, ucn * 8,
+                        aq, xs);
+        start_chunk(kc, ucn);
+        issue_first();
+    }
+    lds_barrier();  // all row sums final
+    for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += kQWg) {
+        const uint32_t row = (t_begin + (i >> 4)) * 16 + (i & 15);
+        if (row < a.rows) y_base[row] = row_sum[i];
+    }
+}
+
+template <int TWO, int DEPTH>
+static const void* iq2_kernel_for(bool route) {
+    return route ? reinterpret_cast<const void*>(&gemv_iq2_kernel<TWO, DEPTH, true>)
+                 : reinterpret_cast<const void*>(&gemv_iq2_kernel<TWO, DEPTH, false>);
+}
+
+static int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
+}  // namespace
+
+hipError_t launch_gemv_iq2(const GemvArgs& a_in, int num_cu, hipStream_t s) {
+    if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
+    GemvArgs a = a_in;
+    // Tuning overrides: MMHIP_IQ2_TWO (0..4 two-table slots per record unit),
+    // MMHIP_IQ2_DEPTH (2 | 3 items in flight per wave).
+    static const int two_env = env_int("MMHIP_IQ2_TWO", -1);
+    static const int depth_env = env_int("MMHIP_IQ2_DEPTH", 0);
+    const int two = (two_env >= 0 && two_env <= 4) ? two_env : 2;
+    const int depth = depth_env == 3 ? 3 : 2;
+    const bool route = a.route_decode != 0;
+    const void* fn;
+    switch (two * 4 + depth) {
+        case 0 * 4 + 2: fn = iq2_kernel_for<0, 2>(route); break;
+        case 0 * 4 + 3: fn = iq2_kernel_for<0, 3>(route); break;
+        case 1 * 4 + 2: fn = iq2_kernel_for<1, 2>(route); break;
+        case 1 * 4 + 3: fn = iq2_kernel_for<1, 3>(route); break;
+        case 2 * 4 + 3: fn = iq2_kernel_for<2, 3>(route); break;
+        case 3 * 4 + 2: fn = iq2_kernel_for<3, 2>(route); break;
+        case 3 * 4 + 3: fn = iq2_kernel_for<3, 3>(route); break;
+        case 4 * 4 + 2: fn = iq2_kernel_for<4, 2>(route); break;
+        case 4 * 4 + 3: fn = iq2_kernel_for<4, 3>(route); break;
+        default: fn = iq2_kernel_for<2, 2>(route); break;
+    }
+    // Tiles per workgroup: the problems' tiles spread over one workgroup per
+    // CU, at most kQMaxTiles (the LDS partials and row sums).
+    const uint64_t total_tiles = (uint64_t)a.n_probs * a.tiles;
+    const uint64_t target = (uint64_t)(num_cu > 0 ? num_cu : 256);
+    uint64_t tpw = (total_tiles + target - 1) / target;
+    if (tpw > kQMaxTiles) tpw = kQMaxTiles;
+    if (tpw > a.tiles) tpw = a.tiles;
+    a.tiles_per_wg = (uint32_t)tpw;
+    dim3 grid((unsigned)((a.tiles + tpw - 1) / tpw), a.n_probs);
+    void* args[] = {&a};
+    return hipLaunchKernel(fn, grid, dim3(kQWg), args, 0, s);
+}
+
+}  // namespace mmhip

@@ -106,6 +106,8 @@ hipError_t launch_quantize(const float* x, uint64_t x_stride, uint32_t n_vec, ui
 // Quantised-weight GEMV over n_probs matrices in one launch (activations are
 // quantised inside the kernel).
 hipError_t launch_gemv_q(const GemvArgs& a, uint32_t fmt, int num_cu, hipStream_t s);
+// IQ2_XXS decode GEMV (gemv_iq2.hip); launch_gemv_q forwards IQ2_XXS here.
+hipError_t launch_gemv_iq2(const GemvArgs& a, int num_cu, hipStream_t s);
 
 // Plain f32 / f16 weight GEMV (router, matVecMulUnified's f32 branch):
 // y_i = W_{first+i} . x_i for i < n_mats.

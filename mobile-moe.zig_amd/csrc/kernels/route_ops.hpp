@@ -201,4 +201,43 @@ __device__ inline TokenRoute route_token(const RouteArgs& a, uint32_t t) {
     return r;
 }
 
+// The routing outputs of a decode call (the single-token branch of the
+// routing kernel): route ids / weights, statistics, slots in route order,
+// the shared slot, and the down problem list. One thread.
+__device__ inline void decode_route_outputs(const RouteArgs& a, const TokenRoute& tr) {
+    const uint32_t E = a.n_experts, k = a.k;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i) {
+        if (a.route_ids) a.route_ids[i] = i < k ? tr.ids[i] : 0xFFFFFFFFu;
+        if (a.route_w) a.route_w[i] = i < k ? tr.w[i] : 0.0f;
+        a.assign_w[i] = ((tr.act >> i) & 1u) ? tr.w[i] : 0.0f;
+        a.assign_slot[i] = -1;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i)
+        if (i < k) atomicAdd(a.counts + tr.ids[i], 1ull);  // stats.record
+    a.deferred[0] = tr.deferred;
+    a.shared_slot[0] = a.shared ? 4 : -1;
+    a.slot_tok[4] = 0;
+    uint32_t s = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i) {
+        if (i >= k || !((tr.act >> i) & 1u)) continue;
+        a.assign_slot[i] = (int32_t)s;
+        a.slot_tok[s] = 0;
+        a.gemv_gu[2 * s] = make_uint4(tr.ids[i], 0, 2 * s, 0);
+        a.gemv_gu[2 * s + 1] = make_uint4(E + tr.ids[i], 0, 2 * s + 1, 0);
+        a.gemv_dn[s] = make_uint4(tr.ids[i], s, s, 0);
+        ++s;
+    }
+    uint32_t n_gu = 2 * s, n_dn = s;
+    if (a.shared && a.shared_merged) {
+        a.gemv_gu[n_gu++] = make_uint4(2 * E, 0, 8, 0);
+        a.gemv_gu[n_gu++] = make_uint4(2 * E + 1, 0, 9, 0);
+        a.gemv_dn[n_dn++] = make_uint4(E, 4, 4, 0);
+    }
+    a.n_gemv[0] = n_gu;
+    a.n_gemv[1] = n_dn;
+}
+
 }  // namespace mmhip
