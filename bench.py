@@ -335,7 +335,7 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": (None if traffic is None else
                         round(traffic["gate_bytes_per_launch"] + traffic["down_bytes_per_launch"])),
-            "kernel": "gemv_q_kernel (IQ2_XXS), one launch per shape",
+            "kernel": "gemv_iq2_kernel, one launch per shape",
             "kernel_us_per_step": round(kernel_us, 3),
             "kernel_us": {"gate_1536x2048": round(g["gate_us"], 3), "down_2048x1536": round(g["down_us"], 3)},
             "bytes_per_step": g["step_bytes"],

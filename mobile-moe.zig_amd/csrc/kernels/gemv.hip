@@ -1,12 +1,12 @@
 // Decode GEMV on gfx950.
 //
-// Quantised weights (Q8_0, IQ2_XXS): a workgroup of 1024 threads (one per CU)
-// owns one activation vector (problem) and a contiguous range of 16-row
-// tiles. It quantises the vector into LDS (the A operand of every MFMA, so the
-// separate quantisation launch disappears), copies the 32 KiB IQ2_XXS
-// sign/grid tables into LDS, and its 16 waves then stream equal shares of the
-// range's 1 KiB record units, one 128-bit load per lane, one step ahead of
-// the compute. Every weight byte is read exactly once.
+// Q8_0 weights: a workgroup (one per CU) owns one activation vector
+// (problem) and a contiguous range of 16-row tiles. It quantises the vector
+// into LDS (the A operand of every MFMA, so the separate quantisation launch
+// disappears), and its waves then stream equal shares of the range's 1 KiB
+// record units, one 128-bit load per lane, steps ahead of the compute. Every
+// weight byte is read exactly once. IQ2_XXS weights have their own kernel
+// (gemv_iq2.hip); launch_gemv_q forwards them there.
 //
 // f32 / f16 weights (the router, matVecMulUnified's f32 branch): one
 // workgroup per output row.
@@ -16,8 +16,6 @@
 #include "tile_ops.hpp"
 
 #include <cstdlib>
-#include <map>
-#include <mutex>
 
 namespace mmhip {
 
@@ -56,18 +54,16 @@ struct StepPos {
 // in flight while LDS is filled. The stream runs one step ahead (two register
 // buffers): the CU's queue holds about one step per wave, and a deeper
 // prefetch only blocks the issuing wave.
-template <int FMT, int UPS, int WG, int DEPTH, bool ROUTE>
+template <int UPS, int WG, int DEPTH, bool ROUTE>
 __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
+    constexpr int FMT = kFmtQ8;
     constexpr uint32_t kWaves = WG / 64;
     constexpr int kRing = DEPTH + 1;  // register buffers: the step computing + DEPTH in flight
-    // Static LDS for the tables (known address: table offsets fold into the
-    // ds_read immediates) and the row sums; dynamic LDS for the activation
-    // chunk.
-    __shared__ __align__(16) uint32_t tab[FMT == kFmtIq2 ? kIq2TableWords : 4];
+    // Static LDS for the row sums; dynamic LDS for the activation chunk.
     __shared__ float row_sum[kGemvMaxTiles * 16];
     __shared__ float edge[2][kWaves * 16];
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr uint32_t kBlkPerUnit = (FMT == kFmtIq2) ? 8 : 2;
+    constexpr uint32_t kBlkPerUnit = 2;
     const uint32_t nblk_all = a.units * kBlkPerUnit;
     const uint32_t chunk_blk = nblk_all < kChunkBlocks ? nblk_all : kChunkBlocks;
     int8_t* aq = reinterpret_cast<int8_t*>(smem);
@@ -138,7 +134,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
         if (valid) {
             const uint32_t t = t_begin + q.t, u = u_begin + q.s * UPS;
             rs = (t * a.units + u) * 1024;
-            ds = (t * 16 * a.d_row + u * (FMT == kFmtIq2 ? 1 : 2)) * 2;
+            ds = (t * 16 * a.d_row + u * 2) * 2;
         }
         load_step<FMT, UPS>(rec_r, rec_voff, rs, d_r, d_voff, ds, r, dw);
     };
@@ -161,10 +157,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     auto compute = [&](uint32_t j, StepPos q, const uint4 (&r)[kMaxUnitsPerStep],
                        const uint32_t (&dw)[kMaxUnitsPerStep]) {
         const uint32_t ub = q.s * UPS;  // unit index within the LDS chunk
-        if (FMT == kFmtIq2)
-            step_dot_iq2<UPS>(r, dw, ub, a_run, has_a, xs_g, tab, acc);
-        else
-            step_dot_q8<UPS>(r, dw, ub, a_run, has_a, xs_g, g, acc);
+        step_dot_q8<UPS>(r, dw, ub, a_run, has_a, xs_g, g, acc);
         const bool tile_end = q.s + 1 == S;
         if (tile_end || j + 1 == j1) {
             const float tot = reduce_groups(acc);
@@ -180,18 +173,16 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     };
 
     {
-        // Prologue: tables, first activation chunk, zeroed row sums.
+        // Prologue: first activation chunk, zeroed row sums.
         const uint32_t nb = chunk_blk;
         const uint32_t xb = min(a.cols, chunk_blk * 32) * 4;
         const BufRsrc x_r = make_rsrc(x, xb);
         const BufRsrc u_r = make_rsrc(x + a.x2_off, silu_mul ? xb : 0);  // zero-size: loads read 0
-        Iq2TableCopy<WG> tc;
-        if (FMT == kFmtIq2) tc.load();
         float xv[4], uv[4];
         x_pass_load(x_r, 0, xv);
         x_pass_load(u_r, 0, uv);
-        // The first weight steps go out now, behind every wave's table and
-        // activation loads (the barrier orders the issue; the CU returns
+        // The first weight steps go out now, behind every wave's activation
+        // loads (the barrier orders the issue; the CU returns
         // loads in issue order), so their HBM latency overlaps the prologue's
         // loads and the LDS fill below; the waits for the prologue data leave
         // them in flight. Activation passes beyond the first (chunks wider
@@ -199,7 +190,6 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
         start_chunk(nb);
         __builtin_amdgcn_s_barrier();
         issue_first();
-        if (FMT == kFmtIq2) tc.store(tab);
         for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) row_sum[i] = 0.0f;
         if (silu_mul) silu_mul4(xv, uv);
         x_pass_store(xv, nb, 0, aq, xs);
@@ -309,17 +299,17 @@ __global__ __launch_bounds__(kFloatThreads) void gemv_float_kernel(const WT* __r
 
 }  // namespace
 
-size_t gemv_q_lds_bytes(uint32_t fmt, uint32_t units) {
-    const uint32_t nblk = units * (fmt == kFmtIq2 ? 8 : 2);
+static size_t gemv_q_lds_bytes(uint32_t units) {
+    const uint32_t nblk = units * 2;
     const uint32_t chunk = nblk < kChunkBlocks ? nblk : kChunkBlocks;
-    return (size_t)((chunk + 7) / 8) * kAGroupBytes + (size_t)chunk * 4;  // tables are static LDS
+    return (size_t)((chunk + 7) / 8) * kAGroupBytes + (size_t)chunk * 4;
 }
 
 // Units per step: a divisor of both the tile's unit count and the LDS
-// chunk's, at most kMaxUnitsPerStep. Q8_0 tiles hold a multiple of 4 units
-// (256-column A groups), and Q8_0 steps are 4 or 8 units.
-static int pick_ups(uint32_t fmt, uint32_t units) {
-    const uint32_t chunk_units = min(units, (uint32_t)(kChunkBlocks / (fmt == kFmtIq2 ? 8 : 2)));
+// chunk's. Q8_0 tiles hold a multiple of 4 units (256-column A groups), and
+// steps are 4 or 8 units.
+static int pick_ups(uint32_t units) {
+    const uint32_t chunk_units = min(units, (uint32_t)(kChunkBlocks / 2));
     uint32_t a = units, b = chunk_units;
     while (b) {
         const uint32_t t = a % b;
@@ -327,28 +317,15 @@ static int pick_ups(uint32_t fmt, uint32_t units) {
         b = t;
     }
     const uint32_t common = a;
-    if (fmt == kFmtIq2) {
-        for (int u = kMaxUnitsPerStep; u >= 1; --u)
-            if (common % u == 0) return u;
-        return 1;
-    }
     if (common % 8 == 0) return 8;
     if (common % 4 == 0) return 4;
     return 0;
 }
 
-template <int FMT, int WG, int DEPTH, bool ROUTE>
+template <int WG, int DEPTH, bool ROUTE>
 static const void* kernel_for(int ups) {
-    switch (ups) {
-        case 1: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 1, WG, DEPTH, ROUTE>);
-        case 2: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 2, WG, DEPTH, ROUTE>);
-        case 3: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 3, WG, DEPTH, ROUTE>);
-        case 4: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 4, WG, DEPTH, ROUTE>);
-        case 5: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 5, WG, DEPTH, ROUTE>);
-        case 6: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 6, WG, DEPTH, ROUTE>);
-        case 7: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 7, WG, DEPTH, ROUTE>);
-        default: return reinterpret_cast<const void*>(&gemv_q_kernel<FMT, 8, WG, DEPTH, ROUTE>);
-    }
+    return ups == 8 ? reinterpret_cast<const void*>(&gemv_q_kernel<8, WG, DEPTH, ROUTE>)
+                    : reinterpret_cast<const void*>(&gemv_q_kernel<4, WG, DEPTH, ROUTE>);
 }
 
 static int env_int(const char* name, int dflt) {
@@ -356,76 +333,44 @@ static int env_int(const char* name, int dflt) {
     return e ? atoi(e) : dflt;
 }
 
-// Resident workgroups per CU of one kernel instance (register and LDS
-// limited), cached per (kernel, LDS bytes).
-static int resident_per_cu(const void* fn, int wg, size_t lds) {
-    static std::mutex mu;
-    static std::map<std::pair<const void*, size_t>, int> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    auto key = std::make_pair(fn, lds);
-    auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
-    int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, wg, lds) != hipSuccess || nb <= 0) nb = 1;
-    cache[key] = nb;
-    return nb;
-}
-
-template <int FMT, int DEPTH>
+template <int DEPTH>
 static const void* kernel_for_wg(int wg, int ups) {
-    if (wg == 256) return kernel_for<FMT, 256, DEPTH, false>(ups);
-    return kernel_for<FMT, 1024, DEPTH, false>(ups);
+    if (wg == 1024) return kernel_for<1024, DEPTH, false>(ups);
+    return kernel_for<256, DEPTH, false>(ups);
 }
 
 hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStream_t s) {
     if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
-    static const bool iq2_old = getenv("MMHIP_IQ2_OLD") != nullptr;
-    if (fmt == kFmtIq2 && !iq2_old) return launch_gemv_iq2(a_in, num_cu, s);
+    if (fmt == kFmtIq2) return launch_gemv_iq2(a_in, num_cu, s);
     GemvArgs a = a_in;
-    // Per-format defaults, measured on MI355X with 64-expert batches:
-    //   IQ2_XXS (decode-bound): 1024 threads, one workgroup per CU (16 waves
-    //     to hide the table and MFMA latencies), one step in flight (a step
-    //     computes long enough to cover the load latency);
-    //   Q8_0 (HBM-bound): 256 threads, one workgroup per CU, two steps in
-    //     flight: four long streams per CU keep fewer requests outstanding
-    //     and reach a higher HBM rate than sixteen.
-    // Overrides: MMHIP_GEMV_WG (256 | 1024), MMHIP_GEMV_MAX_UPS (record units
-    // per step), MMHIP_GEMV_DEPTH (steps in flight, 1..3),
-    // MMHIP_GEMV_WG_PER_CU (workgroups per CU the grid is sized for).
+    // Defaults measured on MI355X with 64-matrix batches: 256 threads, one
+    // workgroup per CU, two steps of 4 units in flight: four long streams
+    // per CU keep fewer requests outstanding and reach a higher HBM rate than
+    // sixteen. Overrides: MMHIP_GEMV_WG (256 | 1024), MMHIP_GEMV_MAX_UPS (4 |
+    // 8 record units per step), MMHIP_GEMV_DEPTH (steps in flight, 1..3).
     static const int wg_env = env_int("MMHIP_GEMV_WG", 0);
     static const int cap_env = env_int("MMHIP_GEMV_MAX_UPS", 0);
     static const int depth_env = env_int("MMHIP_GEMV_DEPTH", 0);
-    static const int wg_per_cu_env = env_int("MMHIP_GEMV_WG_PER_CU", 0);
-    const bool iq2 = fmt == kFmtIq2;
-    int wg = (wg_env == 256 || wg_env == 1024) ? wg_env : (iq2 ? 1024 : 256);
-    // Steps above 4 units exceed the register budget of 4 waves per SIMD
-    // (128 VGPRs with two record buffers) and spill.
-    // The routing variant (decode gate/up) keeps IQ2_XXS steps at 2 units:
-    // its prologue's registers would make 4-unit steps spill.
-    const int cap = (a.route_decode && iq2) ? 2 : (cap_env > 0 ? cap_env : 4);
-    int ups = pick_ups(fmt, a.units);
+    const int wg = wg_env == 1024 ? 1024 : 256;
+    // Steps above 4 units exceed the register budget with two record
+    // buffers in flight and spill.
+    const int cap = cap_env == 8 ? 8 : 4;
+    int ups = pick_ups(a.units);
     if (ups == 0) return hipErrorInvalidValue;
-    while (ups > cap && ups % 2 == 0 && (iq2 || ups > 4)) ups /= 2;
-    int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : (iq2 ? 1 : 2);
+    if (ups > cap) ups = cap;
+    const int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : 2;
     const void* fn;
     if (a.route_decode) {
-        // Decode gate/up with routing in the kernel: the default shapes only.
-        wg = iq2 ? 1024 : 256;
-        depth = iq2 ? 1 : 2;
-        fn = iq2 ? kernel_for<kFmtIq2, 1024, 1, true>(ups) : kernel_for<kFmtQ8, 256, 2, true>(ups);
-    } else if (iq2) {
-        fn = depth == 1 ? kernel_for_wg<kFmtIq2, 1>(wg, ups) : kernel_for_wg<kFmtIq2, 2>(wg, ups);
+        // Decode gate/up with routing in the kernel: the default shape only.
+        fn = kernel_for<256, 2, true>(ups);
     } else {
-        fn = depth == 1   ? kernel_for_wg<kFmtQ8, 1>(wg, ups)
-             : depth == 3 ? kernel_for_wg<kFmtQ8, 3>(wg, ups)
-                          : kernel_for_wg<kFmtQ8, 2>(wg, ups);
+        fn = depth == 1 ? kernel_for_wg<1>(wg, ups) : depth == 3 ? kernel_for_wg<3>(wg, ups) : kernel_for_wg<2>(wg, ups);
     }
-    const size_t lds = gemv_q_lds_bytes(fmt, a.units);
-    const int wg_per_cu = wg_per_cu_env > 0 ? wg_per_cu_env : (iq2 ? resident_per_cu(fn, wg, lds) : 1);
-    // Tiles per workgroup: the problems' tiles spread over every resident
-    // workgroup slot of the device, at most kGemvMaxTiles (the LDS row sums).
+    const size_t lds = gemv_q_lds_bytes(a.units);
+    // Tiles per workgroup: the problems' tiles spread over one workgroup per
+    // CU, at most kGemvMaxTiles (the LDS row sums).
     const uint64_t total_tiles = (uint64_t)a.n_probs * a.tiles;
-    const uint64_t target_wgs = (uint64_t)(num_cu > 0 ? num_cu : 256) * wg_per_cu;
+    const uint64_t target_wgs = (uint64_t)(num_cu > 0 ? num_cu : 256);
     uint64_t tpw = (total_tiles + target_wgs - 1) / target_wgs;
     if (tpw > kGemvMaxTiles) tpw = kGemvMaxTiles;
     if (tpw > a.tiles) tpw = a.tiles;

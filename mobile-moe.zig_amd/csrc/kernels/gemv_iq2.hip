@@ -12,21 +12,20 @@
 // contiguous runs of such pairs, one per wave, so a wave keeps one unit's
 // activation operands in registers while it walks tiles, and the two items
 // of a pair give it two independent MFMA chains. The A operands are sparse: for
-// the MFMA of block s (s = 0..7 within the unit) only the lanes whose A row
-// m = 4j + e belongs to block s hold digits (e = 0/1: hi/lo digits of block j,
-// e = 2/3: of block j + 4), all others hold zero. The eight MFMAs of a unit
+// the 16x16x64 MFMA of blocks 2j, 2j + 1 (lane group g's K range carries
+// the record of sub-block 2j, then that of 2j + 1, both at columns
+// 8g..8g+7) only the lanes whose A row m = 4i + e belongs to one of those
+// blocks hold digits in that block's half (e = 0/1: hi/lo digits of block i,
+// e = 2/3: of block i + 4), all others hold zero. The four MFMAs of a unit
 // accumulate into one result, whose D rows 4g..4g+3 in lane (g, n) are then
 // the hi/lo dot products of blocks g and g + 4 of row n: no cross-lane
 // gather, two digit combines per item, and lane (g, n) scales exactly the two
 // sub-blocks whose ls bits its own record dwords carry.
 //
-// B operands come from LDS tables (record layout in device_common.hpp): the
-// 8-byte table keyed by b012 | P | idx, whose high dword still needs the hi3
-// signs (iq2_fix_hi), or, for the first kTwo even sub-block slots, the low
-// dword from that table and the fully signed high dword from a second 16 KiB
-// table keyed by P | idx | hi3 (record bits 6..17). The two paths trade VALU
-// (sign fix) against LDS bandwidth (a second random read). The table reads
-// of both items of a pair are issued before either is used.
+// B operands come from the 32 KiB LDS table keyed by b012 | P | idx (record
+// layout in device_common.hpp); the hi3 signs of the high dword are applied
+// in registers (iq2_fix_hi). The table reads of both items of a pair are
+// issued before either is used.
 //
 // Each item leaves its 64 lane partial sums in LDS; after a chunk, every
 // output row adds its (unit, lane group) partials in a fixed order, so the
@@ -43,23 +42,7 @@ constexpr int kQWg = 1024;
 constexpr uint32_t kQWaves = kQWg / 64;
 constexpr uint32_t kQChunkUnits = 8;                 // record units per activation chunk
 constexpr uint32_t kQChunkBlocks = kQChunkUnits * 8;  // 32-column blocks per chunk
-constexpr uint32_t kQMaxTiles = 32;                  // row tiles per workgroup
-
-// Second table: entry (P | idx << 1 | hi3 << 9) = columns 4..7 of grid entry
-// idx with signs hi3 (columns 4..6) and P ^ parity(hi3) (column 7, the
-// ksigns parity bit).
-struct Iq2HiTable {
-    uint32_t w[4096];
-};
-constexpr Iq2HiTable make_iq2_hi_table() {
-    Iq2HiTable t{};
-    for (uint32_t e = 0; e < 4096; ++e) {
-        const uint32_t par = e & 1u, idx = (e >> 1) & 0xFFu, hi3 = e >> 9;
-        t.w[e] = negate_bytes((uint32_t)(kIq2Grid[idx] >> 32), nibble_byte_mask(hi3 | ((par ^ parity3(hi3)) << 3)));
-    }
-    return t;
-}
-static __constant__ Iq2HiTable c_iq2_hi = make_iq2_hi_table();
+constexpr uint32_t kQMaxTiles = 48;                  // row tiles per workgroup
 
 // Quantises 4 columns per lane (8 lanes per 32-column block, quantize_quad)
 // into the chunk's digit planes: aq[(b * 2 + digit) * 32 + column].
@@ -138,50 +121,50 @@ struct ItemPos {
 };
 
 // Raw table words of one record unit (lane's 8 records): .x = low dword,
-// .y = high dword (final for two-table slots, hi3 signs still to apply for
-// the others).
+// .y = high dword before the hi3 signs.
 struct RawB {
     uint2 e[8];
 };
 
-template <int TWO>
-__device__ __forceinline__ void fetch_b(const uint4& r, const uint32_t* tab, const uint32_t* hitab, RawB& raw) {
+// Table words of the lane's 8 records (record layout in device_common.hpp):
+// the 8-byte entry keyed by the record's window; its high dword still needs
+// the hi3 signs.
+__device__ __forceinline__ void fetch_b(const uint4& r, const uint32_t* tab, RawB& raw) {
     const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
     const char* t8 = reinterpret_cast<const char*>(tab);
-    const char* th = reinterpret_cast<const char*>(hitab);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         const uint32_t d = w4[s >> 1];
-        if ((s & 1) == 0 && (s >> 1) < TWO) {
-            raw.e[s].x = *reinterpret_cast<const uint32_t*>(t8 + (d & 0x7FF8u));
-            raw.e[s].y = *reinterpret_cast<const uint32_t*>(th + ((d >> 4) & 0x3FFCu));
-        } else {
-            const uint32_t addr = (s & 1) ? ((d >> 15) & 0x7FF8u) : (d & 0x7FF8u);
-            raw.e[s] = *reinterpret_cast<const uint2*>(t8 + addr);
-        }
+        raw.e[s] = *reinterpret_cast<const uint2*>(t8 + ((s & 1) ? ((d >> 15) & 0x7FF8u) : (d & 0x7FF8u)));
     }
 }
 
-template <int TWO>
+// B operands (signed int8 weights, 8 per record) from the table words.
 __device__ __forceinline__ void finish_b(const uint4& r, const RawB& raw, long (&b)[8]) {
     const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         const uint32_t d = w4[s >> 1];
-        uint32_t hi = raw.e[s].y;
-        if (!((s & 1) == 0 && (s >> 1) < TWO)) hi = iq2_fix_hi(hi, (s & 1) ? (d & 7u) : ((d >> 15) & 7u));
+        const uint32_t hi = iq2_fix_hi(raw.e[s].y, (s & 1) ? (d & 7u) : ((d >> 15) & 7u));
         b[s] = (long)(((uint64_t)hi << 32) | (uint64_t)raw.e[s].x);
     }
 }
 
-template <int TWO, int DEPTH, bool ROUTE>
+// B operand of a 16x16x64 MFMA: the records of sub-blocks 2j and 2j + 1
+// (K = 16g..16g+7 and 16g+8..16g+15 of lane group g; the A operand pairs
+// its bytes the same way).
+__device__ __forceinline__ v4i bpair(const long (&b)[8], int j) {
+    const uint64_t l = (uint64_t)b[2 * j], h = (uint64_t)b[2 * j + 1];
+    return v4i{(int)(uint32_t)l, (int)(uint32_t)(l >> 32), (int)(uint32_t)h, (int)(uint32_t)(h >> 32)};
+}
+
+template <int DEPTH, bool ROUTE>
 __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
     constexpr int kRing = DEPTH + 1;
-    // One LDS block with the tables first: their byte offsets (below 48 KiB)
+    // One LDS block with the table first: its byte offsets (below 32 KiB)
     // fold into the ds_read offset fields.
     struct Lds {
         uint32_t tab[kIq2TableWords];
-        uint32_t hitab[TWO > 0 ? 4096 : 4];
         float part[kQChunkUnits * kQMaxTiles * 64];
         uint8_t aq[kQChunkBlocks * 64];
         float xs[kQChunkBlocks];
@@ -189,7 +172,6 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
     };
     __shared__ __align__(16) Lds lds;
     uint32_t* const tab = lds.tab;
-    uint32_t* const hitab = lds.hitab;
     float* const part = lds.part;
     uint8_t* const aq = lds.aq;
     float* const xs = lds.xs;
@@ -198,15 +180,19 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    uint64_t mat, x_row, y_row;
-    if (!select_problem<ROUTE>(a, blockIdx.y, mat, x_row, y_row)) return;  // whole workgroup
+    // The problem: known up front, except in the decode gate/up variant,
+    // which routes the token after its table and activation loads (row 0)
+    // are issued, so the routing overlaps their latency.
+    uint64_t mat = 0, x_row = 0, y_row = 0;
+    if constexpr (!ROUTE) {
+        if (!select_problem<false>(a, blockIdx.y, mat, x_row, y_row)) return;  // whole workgroup
+    }
     const float* x = a.x + x_row * a.x_stride;
-    float* const y_base = a.y + y_row * a.y_stride;
+    float* y_base = nullptr;
     const bool silu_mul = a.silu_mul != 0;
     const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;  // < a.tiles (grid size)
     const uint32_t n_tiles = min(a.tiles - t_begin, a.tiles_per_wg);
-    const BufRsrc rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
-    const BufRsrc d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
+    BufRsrc rec_r, d_r;
     const uint32_t rec_voff = lane * 16;
     const uint32_t d_voff = n * a.d_row * 2;
     // Sparse A row of this lane: block s_star of the unit, digit d_star.
@@ -237,7 +223,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
                 ds = (tile * 16 * a.d_row + u) * 2;
             }
             r[h] = buf_load_b128<kCacheStream>(rec_r, rec_voff, rs);
-            dbits[h] = buf_load_b16<kCacheStream>(d_r, d_voff, ds);
+            dbits[h] = buf_load_b16(d_r, d_voff, ds);  // cached: the tile's other units reuse the line
         }
     };
 
@@ -264,20 +250,23 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
         const BufRsrc x_r = make_rsrc(x, xb);
         const BufRsrc u_r = make_rsrc(x + a.x2_off, silu_mul ? xb : 0);  // zero-size: loads read 0
         const BufRsrc t_r = make_rsrc(&c_iq2_tables, sizeof(Iq2Tables));
-        const BufRsrc h_r = make_rsrc(&c_iq2_hi, sizeof(Iq2HiTable));
-        uint4 tv[2], hv;
+        uint4 tv[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) tv[i] = buf_load_b128(t_r, (threadIdx.x + kQWg * i) * 16, 0);
-        if (TWO > 0) hv = buf_load_b128(h_r, threadIdx.x * 16, 0);
         float xv[4], uv[4];
         x_pass_load(x_r, 0, xv);
         x_pass_load(u_r, 0, uv);
+        if constexpr (ROUTE) {
+            if (!select_problem<true>(a, blockIdx.y, mat, x_row, y_row)) return;  // whole workgroup; x_row stays 0
+        }
+        y_base = a.y + y_row * a.y_stride;
+        rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
+        d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
         start_chunk(0, uc0);
         __builtin_amdgcn_s_barrier();
         issue_first();
 #pragma unroll
         for (int i = 0; i < 2; ++i) reinterpret_cast<uint4*>(tab)[threadIdx.x + kQWg * i] = tv[i];
-        if (TWO > 0) reinterpret_cast<uint4*>(hitab)[threadIdx.x] = hv;
         for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += kQWg) row_sum[i] = 0.0f;
         if (silu_mul) silu_mul4(xv, uv);
         x_store_planes(xv, nb, 0, aq, xs);  // one pass covers 128 >= 64 blocks
@@ -285,7 +274,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
 
     for (uint32_t kc = 0;;) {
         lds_barrier();  // tables, digit planes, scales (and row sums) visible
-        long av[8];
+        v4i av[4];
         float xa = 0.0f, xb = 0.0f, ha = 0.0f, hb = 0.0f;
         uint32_t a_ul = 0xFFFFFFFFu;
         for (uint32_t i = p0; i < p1; i += kRing) {
@@ -299,9 +288,12 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
                         a_ul = cur.ul;
                         const uint8_t* ap = aq + ((a_ul * 8 + s_star) * 2 + d_star) * 32 + 8 * g;
                         const uint2 xw = *reinterpret_cast<const uint2*>(ap);
-                        const long xl = (long)(((uint64_t)xw.y << 32) | (uint64_t)xw.x);
 #pragma unroll
-                        for (int s = 0; s < 8; ++s) av[s] = ((uint32_t)s == s_star) ? xl : 0;
+                        for (int j = 0; j < 4; ++j) {
+                            const bool lo = s_star == 2u * j, hi = s_star == 2u * j + 1;
+                            av[j] = v4i{(int)(lo ? xw.x : 0u), (int)(lo ? xw.y : 0u), (int)(hi ? xw.x : 0u),
+                                        (int)(hi ? xw.y : 0u)};
+                        }
                         xa = xs[a_ul * 8 + g] * 0.25f;
                         xb = xs[a_ul * 8 + g + 4] * 0.25f;
                         ha = xa * 0.5f;
@@ -309,16 +301,16 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
                     }
                     // B operands of both items: all table reads first.
                     RawB raw0, raw1;
-                    fetch_b<TWO>(rb[q][0], tab, hitab, raw0);
-                    fetch_b<TWO>(rb[q][1], tab, hitab, raw1);
+                    fetch_b(rb[q][0], tab, raw0);
+                    fetch_b(rb[q][1], tab, raw1);
                     long b0[8], b1[8];
-                    finish_b<TWO>(rb[q][0], raw0, b0);
-                    finish_b<TWO>(rb[q][1], raw1, b1);
+                    finish_b(rb[q][0], raw0, b0);
+                    finish_b(rb[q][1], raw1, b1);
                     v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
 #pragma unroll
-                    for (int s = 0; s < 8; ++s) {
-                        acc0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[s], b0[s], acc0, 0, 0, 0);
-                        acc1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[s], b1[s], acc1, 0, 0, 0);
+                    for (int j = 0; j < 4; ++j) {
+                        acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], bpair(b0, j), acc0, 0, 0, 0);
+                        acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], bpair(b1, j), acc1, 0, 0, 0);
                     }
                     // Blocks g and g + 4 of row n: d * (0.5 + ls) / 4 * s_x * digits.
 #pragma unroll
@@ -368,10 +360,10 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
     }
 }
 
-template <int TWO, int DEPTH>
+template <int DEPTH>
 static const void* iq2_kernel_for(bool route) {
-    return route ? reinterpret_cast<const void*>(&gemv_iq2_kernel<TWO, DEPTH, true>)
-                 : reinterpret_cast<const void*>(&gemv_iq2_kernel<TWO, DEPTH, false>);
+    return route ? reinterpret_cast<const void*>(&gemv_iq2_kernel<DEPTH, true>)
+                 : reinterpret_cast<const void*>(&gemv_iq2_kernel<DEPTH, false>);
 }
 
 static int env_int(const char* name, int dflt) {
@@ -384,26 +376,10 @@ static int env_int(const char* name, int dflt) {
 hipError_t launch_gemv_iq2(const GemvArgs& a_in, int num_cu, hipStream_t s) {
     if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
     GemvArgs a = a_in;
-    // Tuning overrides: MMHIP_IQ2_TWO (0..4 two-table slots per record unit),
-    // MMHIP_IQ2_DEPTH (2 | 3 items in flight per wave).
-    static const int two_env = env_int("MMHIP_IQ2_TWO", -1);
+    // Pairs in flight per wave: 2 (measured best), MMHIP_IQ2_DEPTH=3 to override.
     static const int depth_env = env_int("MMHIP_IQ2_DEPTH", 0);
-    const int two = (two_env >= 0 && two_env <= 4) ? two_env : 2;
-    const int depth = depth_env == 3 ? 3 : 2;
     const bool route = a.route_decode != 0;
-    const void* fn;
-    switch (two * 4 + depth) {
-        case 0 * 4 + 2: fn = iq2_kernel_for<0, 2>(route); break;
-        case 0 * 4 + 3: fn = iq2_kernel_for<0, 3>(route); break;
-        case 1 * 4 + 2: fn = iq2_kernel_for<1, 2>(route); break;
-        case 1 * 4 + 3: fn = iq2_kernel_for<1, 3>(route); break;
-        case 2 * 4 + 3: fn = iq2_kernel_for<2, 3>(route); break;
-        case 3 * 4 + 2: fn = iq2_kernel_for<3, 2>(route); break;
-        case 3 * 4 + 3: fn = iq2_kernel_for<3, 3>(route); break;
-        case 4 * 4 + 2: fn = iq2_kernel_for<4, 2>(route); break;
-        case 4 * 4 + 3: fn = iq2_kernel_for<4, 3>(route); break;
-        default: fn = iq2_kernel_for<2, 2>(route); break;
-    }
+    const void* fn = (depth_env == 3 && !route) ? iq2_kernel_for<3>(false) : iq2_kernel_for<2>(route);
     // Tiles per workgroup: the problems' tiles spread over one workgroup per
     // CU, at most kQMaxTiles (the LDS partials and row sums).
     const uint64_t total_tiles = (uint64_t)a.n_probs * a.tiles;

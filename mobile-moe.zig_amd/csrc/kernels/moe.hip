@@ -1,6 +1,6 @@
 // MoE routing and combine on gfx950 (moeFFN, inference.zig:886-1010).
 //
-// route_kernel: one workgroup, one wave per token. Each token runs
+// route_kernel: one workgroup, four tokens per wave (one per 16-lane row). Each token runs
 // Scheduler.route exactly as the CPU path does (math.topK's size-k min-heap,
 // softmax over the selected logits, throttle scaling, the heavy-throttle
 // top-1 fallback) and counts its experts (ExpertStats.counts). The workgroup
@@ -20,7 +20,7 @@ namespace mmhip {
 
 namespace {
 
-constexpr int kRouteThreads = 1024;  // 16 waves; one wave per token at a time
+constexpr int kRouteThreads = 1024;  // 16 waves, 4 tokens each at a time
 constexpr int kMaxTokens = 256;      // MMHIP_MOE_MAX_TOKENS
 constexpr int kMaxExperts = 256;
 
@@ -45,7 +45,7 @@ __device__ void route_body(const RouteArgs& a, RouteLds& L) {
     uint32_t* const s_choff = L.choff;
     uint32_t* const s_rank = L.rank;
     const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63, wave = tid >> 6;
+    const uint32_t lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t T = a.n_tokens, E = a.n_experts, k = a.k;
     for (uint32_t e = tid; e < E; e += kRouteThreads) {
         s_cnt[e] = 0;
@@ -53,23 +53,27 @@ __device__ void route_body(const RouteArgs& a, RouteLds& L) {
     }
     __syncthreads();
 
-    for (uint32_t t = wave; t < T; t += kRouteThreads / 64) {
-        const TokenRoute tr = route_token(a, t);
-        const uint32_t act = tr.act, deferred = tr.deferred;
-        const uint32_t(&ids)[kMaxK] = tr.ids;
-        const float(&w)[kMaxK] = tr.w;
-        if (lane == 0) {
-            for (uint32_t i = 0; i < k; ++i) atomicAdd(&s_rec[ids[i]], 1u);  // stats.record (220-222)
+    // Four tokens per wave, one per 16-lane row (route_row16); the row's
+    // first lane writes the token's results.
+    for (uint32_t t0 = 4 * wave; t0 < T; t0 += 4 * (kRouteThreads / 64)) {
+        const uint32_t t = t0 + (lane >> 4);
+        const TokenRoute tr = route_row16(a, t);
+        if ((lane & 15) == 0 && t < T) {
+            const uint32_t act = tr.act;
+#pragma unroll
+            for (uint32_t i = 0; i < kMaxK; ++i)
+                if (i < k) atomicAdd(&s_rec[tr.ids[i]], 1u);  // stats.record (220-222)
             // RouteResult as moeFFN sees it (after the fallback).
+#pragma unroll
             for (uint32_t i = 0; i < kMaxK; ++i) {
-                if (a.route_ids) a.route_ids[t * kMaxK + i] = i < k ? ids[i] : 0xFFFFFFFFu;
-                if (a.route_w) a.route_w[t * kMaxK + i] = i < k ? w[i] : 0.0f;
-                s_ids[t * kMaxK + i] = ids[i];
-                a.assign_w[t * kMaxK + i] = ((act >> i) & 1u) ? w[i] : 0.0f;
+                if (a.route_ids) a.route_ids[t * kMaxK + i] = i < k ? tr.ids[i] : 0xFFFFFFFFu;
+                if (a.route_w) a.route_w[t * kMaxK + i] = i < k ? tr.w[i] : 0.0f;
+                s_ids[t * kMaxK + i] = tr.ids[i];
+                a.assign_w[t * kMaxK + i] = ((act >> i) & 1u) ? tr.w[i] : 0.0f;
                 a.assign_slot[t * kMaxK + i] = -1;
             }
             s_act[t] = act;
-            a.deferred[t] = deferred;
+            a.deferred[t] = tr.deferred;
             a.shared_slot[t] = a.shared ? (int32_t)(4 * T + t) : -1;
             a.slot_tok[4 * T + t] = t;
         }

@@ -69,18 +69,19 @@ __device__ __forceinline__ float score_at(const float (&sc)[4], uint32_t j) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc[3]), l));
 }
 
-__device__ inline void top_k_wave(const float (&sc)[4], uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
-                           float (&ts)[kMaxK]) {
+// math.topK (math.zig:130-174) over scores get(0 .. n-1).
+template <typename Get>
+__device__ inline void top_k_heap(Get get, uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK], float (&ts)[kMaxK]) {
     Heap4 h;
-    h.i0 = 0; h.s0 = score_at(sc, 0);
-    h.i1 = 1; h.s1 = k > 1 ? score_at(sc, 1) : 0.0f;
-    h.i2 = 2; h.s2 = k > 2 ? score_at(sc, 2) : 0.0f;
-    h.i3 = 3; h.s3 = k > 3 ? score_at(sc, 3) : 0.0f;
+    h.i0 = 0; h.s0 = get(0);
+    h.i1 = 1; h.s1 = k > 1 ? get(1) : 0.0f;
+    h.i2 = 2; h.s2 = k > 2 ? get(2) : 0.0f;
+    h.i3 = 3; h.s3 = k > 3 ? get(3) : 0.0f;
     // for (i = k / 2; i > 0;) sift(--i, k)
     if (k / 2 >= 2) h.sift1(k);
     if (k / 2 >= 1) h.sift0(k);
     for (uint32_t j = k; j < n; ++j) {
-        const float v = score_at(sc, j);
+        const float v = get(j);
         if (v > h.s0) {
             h.i0 = j;
             h.s0 = v;
@@ -98,6 +99,26 @@ __device__ inline void top_k_wave(const float (&sc)[4], uint32_t n, uint32_t k, 
         if (ri == 1) { h.i0 = h.i1; h.s0 = h.s1; }
         h.sift0((uint32_t)ri);
     }
+}
+
+// One token per wave: the scores live one per lane (score_at).
+__device__ inline void top_k_wave(const float (&sc)[4], uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
+                                  float (&ts)[kMaxK]) {
+    top_k_heap([&](uint32_t j) { return score_at(sc, j); }, n, k, ids, ts);
+}
+
+// Wave-wide max (every lane receives it) with DPP and the row permutes:
+// within quads, half rows and rows, then across row pairs and halves. All
+// VALU; no LDS round trip. NaN-free inputs (the caller checks).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 
 // The common case of topK without the heap: when the k + 1 largest scores
@@ -134,14 +155,12 @@ __device__ inline bool top_k_distinct(const float (&sc)[4], uint32_t n, uint32_t
                 dup = 1;
             }
         }
-        float m = best_q < 4 ? best : -__builtin_inff();
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        const float m = wave_max(best_q < 4 ? best : -__builtin_inff());
         const bool mine = best_q < 4 && best == m;
         const unsigned long long who = __ballot(mine);
         if (__popcll(who) != 1 || __any(mine && dup)) return false;
         const uint32_t wl = (uint32_t)__builtin_ctzll(who);
-        const uint32_t wq = (uint32_t)__shfl((int)best_q, (int)wl, 64);
+        const uint32_t wq = (uint32_t)__builtin_amdgcn_readlane((int)best_q, (int)wl);
         if (r < k) {
             ids[r] = wl + 64 * wq;
             ts[r] = m;
@@ -159,16 +178,19 @@ struct TokenRoute {
     float w[kMaxK];
     uint32_t act, deferred;
 };
-__device__ inline TokenRoute route_token(const RouteArgs& a, uint32_t t) {
+// Router scores of token t, lane l holding experts l, l + 64, l + 128, l + 192
+// (experts past n_experts read as zero and are never selected).
+__device__ inline void load_scores(const RouteArgs& a, uint32_t t, float (&sc)[4]) {
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t E = a.n_experts, k = a.k;
-    const BufRsrc sr = make_rsrc(a.scores + (uint64_t)t * E, E * 4);
-    float sc[4];
+    const BufRsrc sr = make_rsrc(a.scores + (uint64_t)t * a.n_experts, a.n_experts * 4);
 #pragma unroll
     for (int q = 0; q < 4; ++q) sc[q] = __uint_as_float(buf_load_b32(sr, (lane + 64 * q) * 4, 0));
-    TokenRoute r{{0, 0, 0, 0}, {0.f, 0.f, 0.f, 0.f}, 0, 0};
-    float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f};
-    if (!top_k_distinct(sc, E, k, r.ids, ts)) top_k_wave(sc, E, k, r.ids, ts);
+}
+
+// Route weights of the selected experts (ids, logits ts in topK order).
+__device__ inline TokenRoute finish_route(const RouteArgs& a, const uint32_t (&ids)[kMaxK], const float (&ts)[kMaxK]) {
+    const uint32_t k = a.k;
+    TokenRoute r{{ids[0], ids[1], ids[2], ids[3]}, {0.f, 0.f, 0.f, 0.f}, 0, 0};
     // Softmax over the selected logits, then the routed scaling factor
     // (scheduler.zig:184-201). Loops run over kMaxK with a k test so that
     // every array index is a compile-time constant (registers, no scratch).
@@ -199,6 +221,105 @@ __device__ inline TokenRoute route_token(const RouteArgs& a, uint32_t t) {
         if (rem > 0.0f) r.w[0] = r.w[0] * (a.scale / rem);
     }
     return r;
+}
+
+// Routing of one token by a whole wave (scores one per lane).
+__device__ inline TokenRoute route_scores(const RouteArgs& a, const float (&sc)[4]) {
+    uint32_t ids[kMaxK] = {0, 0, 0, 0};
+    float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f};
+    if (!top_k_distinct(sc, a.n_experts, a.k, ids, ts)) top_k_wave(sc, a.n_experts, a.k, ids, ts);
+    return finish_route(a, ids, ts);
+}
+
+// Routing of 4 tokens per wave, one per 16-lane row: lane p of a row holds
+// the token's scores p, p + 16, ..., p + 240 (experts past n_experts are
+// never selected). k + 1 rounds of a row-wide max pick the selected experts
+// as top_k_distinct does, all rows at once; a row whose k + 1 largest scores
+// are not distinct, or that holds a NaN, is routed by math.topK's heap over
+// the token's scores in memory instead (exact insertion order), by the row's
+// first lane. t is the row's token; rows with t >= n_tokens do nothing useful.
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ uint32_t row_max16u(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+    return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+}
+
+__device__ inline TokenRoute route_row16(const RouteArgs& a, uint32_t t) {
+    const uint32_t lane = threadIdx.x & 63, p = lane & 15, row = lane >> 4;
+    const uint32_t E = a.n_experts, k = a.k;
+    const bool live = t < a.n_tokens;
+    const BufRsrc sr = make_rsrc(a.scores + (uint64_t)(live ? t : 0) * E, live ? E * 4 : 0);
+    float sc[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) sc[c] = __uint_as_float(buf_load_b32(sr, (p + 16 * c) * 4, 0));
+    uint32_t valid = 0;
+    bool bad = false;
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+        if (p + 16 * c < E) {
+            valid |= 1u << c;
+            bad |= sc[c] != sc[c];
+        }
+    uint32_t ids[kMaxK] = {0, 0, 0, 0};
+    float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t rounds = k < E ? k + 1 : k;
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxK + 1; ++r) {  // constant r: ids / ts stay in registers
+        if (r >= rounds) break;
+        float best = -__builtin_inff();
+        uint32_t bc = 16, dup = 0;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            if (!((valid >> c) & 1u)) continue;
+            if (bc == 16 || sc[c] > best) {
+                best = sc[c];
+                bc = c;
+                dup = 0;
+            } else if (sc[c] == best) {
+                dup = 1;
+            }
+        }
+        const float m = row_max16(bc < 16 ? best : -__builtin_inff());
+        const bool mine = bc < 16 && best == m;
+        const unsigned long long who = __ballot(mine);
+        const uint32_t in_row = (uint32_t)(who >> (16 * row)) & 0xFFFFu;
+        if (__builtin_popcount(in_row) != 1 || (mine && dup)) bad = true;
+        const uint32_t id = row_max16u(mine ? p + 16 * bc + 1 : 0u) - 1u;
+        if (r < k) {
+            ids[r] = id;
+            ts[r] = m;
+        }
+        if (mine) valid &= ~(1u << bc);
+    }
+    // A row is bad when any of its lanes saw a clash.
+    const unsigned long long bad_rows = __ballot(bad);
+    if ((bad_rows >> (16 * row)) & 0xFFFFu) {
+        // Exact heap over the token's scores, by the row's first lane.
+        if (p == 0 && live) {
+            const float* srow = a.scores + (uint64_t)t * E;
+            top_k_heap([&](uint32_t j) { return srow[j]; }, E, k, ids, ts);
+        }
+        // Row-uniform again: lane 16 row holds the result.
+#pragma unroll
+        for (int i = 0; i < kMaxK; ++i) {
+            ids[i] = (uint32_t)__shfl((int)ids[i], (int)(16 * row), 64);
+            ts[i] = __shfl(ts[i], (int)(16 * row), 64);
+        }
+    }
+    return finish_route(a, ids, ts);
+}
+
+__device__ inline TokenRoute route_token(const RouteArgs& a, uint32_t t) {
+    float sc[4];
+    load_scores(a, t, sc);
+    return route_scores(a, sc);
 }
 
 // The routing outputs of a decode call (the single-token branch of the

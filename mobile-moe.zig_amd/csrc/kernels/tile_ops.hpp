@@ -84,44 +84,6 @@ __device__ __forceinline__ uint32_t iq2_scale_bits(const uint32_t (&dw)[kMaxUnit
     return dw[i];
 }
 
-// One decode step of UPS record units (compile-time, fully unrolled).
-// IQ2_XXS: unit i is 256-column group ub + i of the LDS activation chunk.
-// Only lanes n = 0, 1 (A rows 0 / 1) carry activation digits; the other
-// lanes' A rows only reach D rows that are never read, so they skip the LDS
-// reads (exec-masked) and keep whatever their registers hold. The B operands
-// of unit i+1 are read from LDS before the MFMAs of unit i issue, so table
-// latency overlaps MFMA and VALU work. xs_g = xs + g.
-template <int UPS>
-__device__ __forceinline__ void step_dot_iq2(const uint4 (&r)[kMaxUnitsPerStep],
-                                             const uint32_t (&dw)[kMaxUnitsPerStep], uint32_t ub,
-                                             const int8_t* a_run, bool has_a, const float* xs_g,
-                                             const uint32_t* tab, float& acc) {
-    long b[2][8];
-    long av[8];
-    iq2_decode_unit(r[0], tab, b[0]);
-#pragma unroll
-    for (int i = 0; i < UPS; ++i) {
-        const int cur = i & 1, nxt = cur ^ 1;
-        if (has_a) lds_a_group(av, a_run, ub + i);
-        if (i + 1 < UPS) iq2_decode_unit(r[i + 1], tab, b[nxt]);
-        const uint32_t blk0 = (ub + i) * 8;
-        int v[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const v4i dv = mfma_i8(av[s], b[cur][s]);
-            v[s] = digits_combine(dv[0], dv[1]);
-        }
-        const int w0 = gather_rows4(v[0], v[1], v[2], v[3]);
-        const int w1 = gather_rows4(v[4], v[5], v[6], v[7]);
-        const float dq = f16_scale(iq2_scale_bits<UPS>(dw, i)) * 0.25f;
-        const float hdq = dq * 0.5f;
-        const float c0 = fmaf((float)iq2_ls_a(r[i]), dq, hdq) * xs_g[blk0];
-        const float c1 = fmaf((float)iq2_ls_b(r[i]), dq, hdq) * xs_g[blk0 + 4];
-        acc = fmaf((float)w0, c0, acc);
-        acc = fmaf((float)w1, c1, acc);
-    }
-}
-
 // Q8_0: units in pairs (four 32-column blocks per gather); a pair is half of
 // a 256-column A group. UPS is 4 or 8 and ub a multiple of 4, so steps start
 // on A-group boundaries.
