@@ -306,7 +306,8 @@ int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float*
     QuantAct q = quant_act_view(qscratch->p, batch, g.cols_pad);
     {
         TimedLaunch tl(ctx, "quantize");
-        e = launch_quantize(x, w->cols, (uint32_t)batch, (uint32_t)w->cols, (uint32_t)g.cols_pad, q, ctx->stream);
+        e = launch_quantize(x, w->cols, (uint32_t)batch, (uint32_t)w->cols, (uint32_t)g.cols_pad, q, ctx->stream,
+                            g.fmt == kFmtIq2);
     }
     if (e != hipSuccess) return hip_fail(e, "qmm: quantize");
     const uint64_t ld = out_layout == 0 ? w->rows : batch;

@@ -178,6 +178,39 @@ __global__ void quantize_silu_kernel(const float* __restrict__ src, uint64_t src
     if (j == 0) sc[v * s_stride + b] = s;
 }
 
+// Wide variants: one wave per 256-column unit (4 columns per lane), one
+// scale per unit stored into the unit's eight block slots. src_stride /
+// u_off as quantize_silu_kernel; silu == 0: plain quantisation of x.
+template <bool SILU>
+__global__ __launch_bounds__(256) void quantize_wide_kernel(const float* __restrict__ src, uint64_t src_stride,
+                                                             uint64_t u_off, const uint32_t* __restrict__ n_rows,
+                                                             uint32_t n_max, uint32_t cols, uint32_t cols_pad,
+                                                             int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                             float* __restrict__ sc, uint64_t q_stride,
+                                                             uint64_t s_stride) {
+    const uint32_t nunit = cols_pad / 256;
+    const uint64_t unit = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t rows = n_rows ? min(*n_rows, n_max) : n_max;
+    if (unit >= (uint64_t)rows * nunit) return;  // whole wave exits together
+    const uint64_t v = unit / nunit;
+    const uint32_t u = (uint32_t)(unit % nunit);
+    const uint32_t c0 = u * 256 + lane * 4;
+    const float* g = src + v * src_stride;
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t col = c0 + e;
+        x[e] = 0.0f;
+        if (col < cols) x[e] = SILU ? silu(g[col]) * g[u_off + col] : g[col];
+    }
+    uint32_t h4, l4;
+    const float s = quantize_quad_wave(x, h4, l4);
+    *reinterpret_cast<uint32_t*>(hi + v * q_stride + c0) = h4;
+    *reinterpret_cast<uint32_t*>(lo + v * q_stride + c0) = l4;
+    if (lane < 8) sc[v * s_stride + u * 8 + lane] = s;
+}
+
 }  // namespace
 
 hipError_t launch_dequant(const void* raw, uint32_t type, uint64_t n, float* out, hipStream_t s) {
@@ -220,10 +253,16 @@ hipError_t launch_repack(const void* raw, const TileGeom& g, uint4* recs, uint16
 }
 
 hipError_t launch_quantize(const float* x, uint64_t x_stride, uint32_t n_vec, uint32_t cols,
-                           uint32_t cols_pad, const QuantAct& q, hipStream_t s) {
+                           uint32_t cols_pad, const QuantAct& q, hipStream_t s, bool wide) {
     uint64_t threads = (uint64_t)n_vec * cols_pad;
     if (threads == 0) return hipSuccess;
     const int bs = 256;
+    if (wide) {
+        if (cols_pad % 256) return hipErrorInvalidValue;
+        quantize_wide_kernel<false><<<(unsigned)((threads / 4 + bs - 1) / bs), bs, 0, s>>>(
+            x, x_stride, 0, nullptr, n_vec, cols, cols_pad, q.hi, q.lo, q.scale, q.stride, q.scale_stride);
+        return hipGetLastError();
+    }
     quantize_kernel<<<(unsigned)((threads + bs - 1) / bs), bs, 0, s>>>(
         x, x_stride, n_vec, cols, cols_pad, q.hi, q.lo, q.scale, q.stride, q.scale_stride);
     return hipGetLastError();
@@ -231,10 +270,17 @@ hipError_t launch_quantize(const float* x, uint64_t x_stride, uint32_t n_vec, ui
 
 hipError_t launch_quantize_silu(const float* src, uint64_t src_stride, uint64_t u_off, const uint32_t* n_rows,
                                 uint32_t n_rows_max, uint32_t cols, uint32_t cols_pad, const QuantAct& q,
-                                hipStream_t s) {
+                                hipStream_t s, bool wide) {
     const uint64_t threads = (uint64_t)n_rows_max * cols_pad;
     if (threads == 0) return hipSuccess;
     const int bs = 256;
+    if (wide) {
+        if (cols_pad % 256) return hipErrorInvalidValue;
+        quantize_wide_kernel<true><<<(unsigned)((threads / 4 + bs - 1) / bs), bs, 0, s>>>(
+            src, src_stride, u_off, n_rows, n_rows_max, cols, cols_pad, q.hi, q.lo, q.scale, q.stride,
+            q.scale_stride);
+        return hipGetLastError();
+    }
     quantize_silu_kernel<<<(unsigned)((threads + bs - 1) / bs), bs, 0, s>>>(
         src, src_stride, u_off, n_rows, n_rows_max, cols, cols_pad, q.hi, q.lo, q.scale, q.stride, q.scale_stride);
     return hipGetLastError();

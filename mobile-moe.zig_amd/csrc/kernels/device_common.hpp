@@ -297,6 +297,20 @@ __device__ __forceinline__ float quantize_block32(float x, int8_t* hi, int8_t* l
     return scale;
 }
 
+// Wave-wide max (every lane receives it) with DPP and the row permutes:
+// within quads, half rows and rows, then across row pairs and halves. All
+// VALU; no LDS round trip. NaN-free inputs (the caller checks).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
 // Max over each aligned group of 8 lanes (DPP: quad swaps, then the
 // half-row mirror); every lane of the group receives it. All 64 lanes must be
 // active.
@@ -320,6 +334,40 @@ __device__ __forceinline__ float quantize_quad(const float (&v)[4], uint32_t& hi
 #pragma unroll
     for (int e = 0; e < 4; ++e) m = fmaxf(m, (v[e] != v[e]) ? __uint_as_float(0x7F800000u) : fabsf(v[e]));
     m = max8_lanes(m);
+    float scale, inv;
+    if (!(m <= 3.4028235e38f)) {
+        scale = __uint_as_float(0x7FC00000u);
+        inv = 0.0f;
+    } else if (m < 0x1p-100f) {
+        scale = 0.0f;
+        inv = 0.0f;
+    } else {
+        scale = m * (1.0f / kDigitMax);
+        inv = __builtin_amdgcn_rcpf(scale);
+    }
+    hi4 = 0;
+    lo4 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float qf = fminf(fmaxf(rintf(v[e] * inv), -kDigitMax), kDigitMax);
+        const int q = (inv == 0.0f) ? 0 : (int)qf;
+        const int h = (q + 128) >> 8;
+        const int l = q - h * 256;
+        hi4 |= (uint32_t)(h & 0xFF) << (8 * e);
+        lo4 |= (uint32_t)(l & 0xFF) << (8 * e);
+    }
+    return scale;
+}
+
+// Quantisation of 4 columns per lane with one scale for the whole wave
+// (256 columns): the block fixed point of quantize_quad with the max taken
+// over 64 lanes. Used where the consumer applies one activation scale per
+// 256-column record unit (the grouped IQ2_XXS matmul).
+__device__ __forceinline__ float quantize_quad_wave(const float (&v)[4], uint32_t& hi4, uint32_t& lo4) {
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m = fmaxf(m, (v[e] != v[e]) ? __uint_as_float(0x7F800000u) : fabsf(v[e]));
+    m = wave_max(m);
     float scale, inv;
     if (!(m <= 3.4028235e38f)) {
         scale = __uint_as_float(0x7FC00000u);

@@ -62,6 +62,12 @@ __device__ __forceinline__ void lds_a_pair(const uint8_t* aq, uint32_t pair, uin
 
 // One step of UPS IQ2_XXS units (unit u = 256 columns = 4 block pairs) for 8
 // activation rows; xs_lds[j * nb + b] = scale of row j, block b of the chunk.
+// The activations carry one scale per unit (quantised wide), so a unit's
+// value for row n and activation row j is
+//   d_n / 8 * s_j * sum_s (2 ls_ns + 1) * (256 D_hi,s + D_lo,s)
+// (dequant.zig:336: d * (0.5 + ls) / 4): the eight blocks' digit dot products
+// are weighted by 2 ls + 1 and summed exactly in int32 (24-bit multiplies:
+// |D| <= 32 * 128 * 43, weighted sums < 2^26), then converted and scaled once.
 template <int UPS>
 __device__ __forceinline__ void step_group_iq2(const uint4 (&r)[kMaxUnitsPerStep], const uint32_t (&dw)[kMaxUnitsPerStep],
                                                uint32_t ub, const uint8_t* aq, const float* xs0, const float* xs1,
@@ -76,23 +82,22 @@ __device__ __forceinline__ void step_group_iq2(const uint4 (&r)[kMaxUnitsPerStep
 #pragma unroll
         for (int q = 0; q < 4; ++q) lds_a_pair(aq, (ub + i) * 4 + q, lane, av[2 * q], av[2 * q + 1]);
         const uint32_t blk0 = (ub + i) * 8;
-        const float4 x0a = *reinterpret_cast<const float4*>(xs0 + blk0);
-        const float4 x0b = *reinterpret_cast<const float4*>(xs0 + blk0 + 4);
-        const float4 x1a = *reinterpret_cast<const float4*>(xs1 + blk0);
-        const float4 x1b = *reinterpret_cast<const float4*>(xs1 + blk0 + 4);
-        const float x0[8] = {x0a.x, x0a.y, x0a.z, x0a.w, x0b.x, x0b.y, x0b.z, x0b.w};
-        const float x1[8] = {x1a.x, x1a.y, x1a.z, x1a.w, x1b.x, x1b.y, x1b.z, x1b.w};
+        const float x0 = xs0[blk0], x1 = xs1[blk0];
         const uint32_t ls = iq2_ls_all(r[i], g);
         if (i + 1 < UPS) iq2_decode_unit(r[i + 1], tab, b[nxt]);
-        const float dq = f16_scale(iq2_scale_bits<UPS>(dw, i)) * 0.25f;
-        const float hdq = dq * 0.5f;
+        int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const v4i dv = mfma_i8(av[s], b[cur][s]);
-            const float ws = fmaf((float)((ls >> (4 * s)) & 15u), dq, hdq);
-            acc0 = fmaf((float)digits_combine(dv[0], dv[1]), ws * x0[s], acc0);
-            acc1 = fmaf((float)digits_combine(dv[2], dv[3]), ws * x1[s], acc1);
+            const int t = (int)(((ls >> (4 * s)) & 15u) * 2 + 1);
+            h0 = __mul24(dv[0], t) + h0;
+            l0 = __mul24(dv[1], t) + l0;
+            h1 = __mul24(dv[2], t) + h1;
+            l1 = __mul24(dv[3], t) + l1;
         }
+        const float c = f16_scale(iq2_scale_bits<UPS>(dw, i)) * 0.125f;
+        acc0 = fmaf(fmaf((float)h0, 256.0f, (float)l0), c * x0, acc0);
+        acc1 = fmaf(fmaf((float)h1, 256.0f, (float)l1), c * x1, acc1);
     }
 }
 

@@ -99,9 +99,11 @@ hipError_t launch_dequant(const void* raw, uint32_t ggml_type, uint64_t n, float
 hipError_t launch_repack(const void* raw, const TileGeom& g, uint4* recs, uint16_t* dvals, hipStream_t s);
 
 // x [n_vec][cols] (row stride x_stride floats) -> digits + scales; columns in
-// [cols, cols_pad) are written as zero.
+// [cols, cols_pad) are written as zero. wide: one scale per 256 columns,
+// repeated in the unit's eight block slots (cols_pad a multiple of 256; the
+// grouped IQ2_XXS matmul requires it).
 hipError_t launch_quantize(const float* x, uint64_t x_stride, uint32_t n_vec, uint32_t cols,
-                           uint32_t cols_pad, const QuantAct& q, hipStream_t s);
+                           uint32_t cols_pad, const QuantAct& q, hipStream_t s, bool wide = false);
 
 // Quantised-weight GEMV over n_probs matrices in one launch (activations are
 // quantised inside the kernel).
@@ -132,7 +134,7 @@ hipError_t launch_group_experts(const uint4* recs, const uint16_t* dvals, const 
 // n_rows is null): g = src + r * src_stride, u = g + u_off.
 hipError_t launch_quantize_silu(const float* src, uint64_t src_stride, uint64_t u_off, const uint32_t* n_rows,
                                 uint32_t n_rows_max, uint32_t cols, uint32_t cols_pad, const QuantAct& q,
-                                hipStream_t s);
+                                hipStream_t s, bool wide = false);
 
 // ---- MoE routing and combine (moe.hip) ----
 //

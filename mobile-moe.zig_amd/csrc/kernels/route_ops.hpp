@@ -107,20 +107,6 @@ __device__ inline void top_k_wave(const float (&sc)[4], uint32_t n, uint32_t k, 
     top_k_heap([&](uint32_t j) { return score_at(sc, j); }, n, k, ids, ts);
 }
 
-// Wave-wide max (every lane receives it) with DPP and the row permutes:
-// within quads, half rows and rows, then across row pairs and halves. All
-// VALU; no LDS round trip. NaN-free inputs (the caller checks).
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
-    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
-}
-
 // The common case of topK without the heap: when the k + 1 largest scores
 // are distinct (and no score is NaN), the heap's result is exactly those k in
 // descending order. k + 1 rounds of a wave-wide max find them; a repeated

@@ -241,7 +241,10 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
         const QuantAct qh = quant_act_view(L->xq_h, T, gg.cols_pad);
         {
             TimedLaunch tl(ctx, "moe_quantize");
-            MOE_TRY(check_hip(launch_quantize(hidden, H, T, H, (uint32_t)gg.cols_pad, qh, s), "moe: quantize"));
+            // One activation scale per 256 columns when an IQ2_XXS grouped
+            // matmul reads the digits (routed experts or the shared expert).
+            const bool wide = gg.fmt == kFmtIq2 || (sep_shared && L->sh_gu->geom.fmt == kFmtIq2);
+            MOE_TRY(check_hip(launch_quantize(hidden, H, T, H, (uint32_t)gg.cols_pad, qh, s, wide), "moe: quantize"));
         }
         {
             TimedLaunch tl(ctx, "moe_gateup");
@@ -266,7 +269,7 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
         {
             TimedLaunch tl(ctx, "moe_quantize");
             MOE_TRY(check_hip(launch_quantize_silu(L->y_gu, 2 * (uint64_t)I, I, nullptr, 5 * T, I, (uint32_t)gd.cols_pad,
-                                                   qd, s),
+                                                   qd, s, gd.fmt == kFmtIq2),
                               "moe: silu quantize"));
         }
         {
@@ -278,7 +281,7 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
                 const TileGeom& gs = L->sh_dn->geom;
                 const QuantAct qs = quant_act_view(L->xq_sd, T, gs.cols_pad);
                 MOE_TRY(check_hip(launch_quantize_silu(L->y_sh, 2 * (uint64_t)SI, SI, nullptr, T, SI,
-                                                       (uint32_t)gs.cols_pad, qs, s),
+                                                       (uint32_t)gs.cols_pad, qs, s, gs.fmt == kFmtIq2),
                                   "moe: shared silu quantize"));
                 MOE_TRY(check_hip(launch_group_dense(L->sh_dn->recs, L->sh_dn->dvals, gs, 0, qs, T,
                                                      L->eo + 4 * (uint64_t)T * H, H, 0, ctx->num_cu, s),
