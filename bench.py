@@ -170,7 +170,12 @@ def zipf_batch(rng, t, s=1.1):
     return h, router
 
 
-def moe_section(ctx, ev, rng, calls, n_layers=4):
+def moe_section(ctx, ev, rng, calls, n_layers=8, n_tokens=61):
+    """MoE layer µs/token. Cold: calls rotate over n_layers layers (each with its
+    own 64 experts, 158 MB) and, at batch 1, over n_tokens distinct tokens, so
+    the routed experts change from call to call and the touched weights
+    (about 0.6 GB at batch 1, 1 GB at batch 64) exceed the 256 MB
+    Infinity Cache. Warm: one layer and one input repeated."""
     router, gate, up, down, shared = moe_weights(rng)
     h64, id_router = zipf_batch(rng, 64)
     kw = dict(hidden=HIDDEN, inter=INTER, n_experts=EXPERTS, expert_type=mm.IQ2_XXS, gate=gate, up=up, down=down,
@@ -178,22 +183,33 @@ def moe_section(ctx, ev, rng, calls, n_layers=4):
     dec = [mm.MoeLayer(ctx, router=router, **kw) for _ in range(n_layers)]
     pre = [mm.MoeLayer(ctx, router=id_router, **kw) for _ in range(n_layers)]
     stream = ctx.stream
-    out = {}
-    for t, layers, h in ((1, dec, rng.standard_normal((1, HIDDEN)).astype(np.float32)), (64, pre, h64)):
-        hd = mm.DeviceArray.from_numpy(ctx, h)
-        od = mm.DeviceArray(ctx, h.nbytes)
-        for i in range(10):
-            layers[i % n_layers].ffn_dev(hd, od, t)
-        ctx.synchronize()
+    toks = rng.standard_normal((n_tokens, HIDDEN)).astype(np.float32)
+    cases = ((1, dec, [mm.DeviceArray.from_numpy(ctx, toks[j:j + 1]) for j in range(n_tokens)]),
+             (64, pre, [mm.DeviceArray.from_numpy(ctx, h64)]))
+    out, warm = {}, {}
+    for t, layers, hs in cases:
+        od = mm.DeviceArray(ctx, t * HIDDEN * 4)
         n = calls if t == 1 else max(10, calls // 4)
-        ms = ev.time_ms(stream, lambda: [layers[i % n_layers].ffn_dev(hd, od, t) for i in range(n)]) / n
-        out[t] = ms * 1e3 / t
-        hd.free()
+        n = max(n, 2 * n_layers)
+
+        def run(i):
+            layers[i % n_layers].ffn_dev(hs[i % len(hs)], od, t)
+
+        for i in range(2 * n_layers):
+            run(i)
+        ctx.synchronize()
+        out[t] = ev.time_ms(stream, lambda: [run(i) for i in range(n)]) / n * 1e3 / t
+        for _ in range(5):
+            layers[0].ffn_dev(hs[0], od, t)
+        ctx.synchronize()
+        warm[t] = ev.time_ms(stream, lambda: [layers[0].ffn_dev(hs[0], od, t) for _ in range(n)]) / n * 1e3 / t
+        for h in hs:
+            h.free()
         od.free()
     touched = len(set(np.argsort(-h64[:, :EXPERTS], axis=1)[:, :4].reshape(-1).tolist()))
     for layer in dec + pre:
         layer.free()
-    return out, touched, (router, gate, up, down, shared, h64, id_router)
+    return out, warm, touched, (router, gate, up, down, shared, h64, id_router)
 
 
 def cpu_gemv_baseline(seconds):
@@ -346,11 +362,13 @@ def main():
     }
     weights = None
     if not args.no_moe:
-        moe, touched, weights = moe_section(ctx, ev, rng, max(50, args.steps))
+        moe, warm, touched, weights = moe_section(ctx, ev, rng, max(50, args.steps))
         out["moe"] = {"batch1_us_per_token": round(moe[1], 3), "batch64_us_per_token": round(moe[64], 3),
+                      "batch1_warm_us_per_token": round(warm[1], 3), "batch64_warm_us_per_token": round(warm[64], 3),
                       "unit": "µs/token", "experts_touched_batch64": touched,
                       "workload": "hidden 2048, 64 IQ2_XXS experts (1536) top-4 + shared, f32 router; "
-                                  "batch 64 with Zipf(1.1) routing; four layers rotate (cold weights)"}
+                                  "batch 64 with Zipf(1.1) routing; cold: eight layers rotate (batch 1 also over "
+                                  "61 tokens); warm: one layer, one input"}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_gemv_baseline(args.cpu_seconds)
         if weights is not None:

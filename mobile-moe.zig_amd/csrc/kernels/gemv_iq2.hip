@@ -380,14 +380,26 @@ hipError_t launch_gemv_iq2(const GemvArgs& a_in, int num_cu, hipStream_t s) {
     static const int depth_env = env_int("MMHIP_IQ2_DEPTH", 0);
     const bool route = a.route_decode != 0;
     const void* fn = (depth_env == 3 && !route) ? iq2_kernel_for<3>(false) : iq2_kernel_for<2>(route);
-    // Tiles per workgroup: the problems' tiles spread over one workgroup per
-    // CU, at most kQMaxTiles (the LDS partials and row sums).
-    const uint64_t total_tiles = (uint64_t)a.n_probs * a.tiles;
-    const uint64_t target = (uint64_t)(num_cu > 0 ? num_cu : 256);
-    uint64_t tpw = (total_tiles + target - 1) / target;
-    if (tpw > kQMaxTiles) tpw = kQMaxTiles;
-    if (tpw > a.tiles) tpw = a.tiles;
-    a.tiles_per_wg = (uint32_t)tpw;
+    // Tiles per workgroup (at most kQMaxTiles: the LDS partials and row
+    // sums). One workgroup fits a CU, so a grid of W workgroups runs in
+    // ceil(W / CUs) rounds; the choice minimises rounds x (tiles x units x
+    // per-item time + per-workgroup fixed time), with the costs measured on
+    // MI355X (~65 ns per 1 KiB item per CU, ~2 us of prologue and tail).
+    // E.g. 10 matrices of 128 tiles take 6 tiles per workgroup (220
+    // workgroups, one round) rather than 5 (260, two rounds).
+    const uint64_t cus = (uint64_t)(num_cu > 0 ? num_cu : 256);
+    const uint32_t max_tpw = a.tiles < kQMaxTiles ? a.tiles : kQMaxTiles;
+    uint32_t tpw = max_tpw;
+    double best = 0.0;
+    for (uint32_t t = 1; t <= max_tpw; ++t) {
+        const uint64_t wgs = (uint64_t)a.n_probs * ((a.tiles + t - 1) / t);
+        const double cost = (double)((wgs + cus - 1) / cus) * ((double)t * a.units * 0.065 + 2.0);
+        if (t == 1 || cost < best) {
+            best = cost;
+            tpw = t;
+        }
+    }
+    a.tiles_per_wg = tpw;
     dim3 grid((unsigned)((a.tiles + tpw - 1) / tpw), a.n_probs);
     void* args[] = {&a};
     return hipLaunchKernel(fn, grid, dim3(kQWg), args, 0, s);

@@ -142,6 +142,23 @@ def test_token_counts(ctx, orc, t):
         gpu.free()
 
 
+@pytest.mark.parametrize("shared_inter", [256, 512])
+def test_decode_calls_in_a_row(ctx, orc, shared_inter):
+    """Decode calls back to back on one layer, a prefill call and a heavy-throttle
+    call (one routed expert) in between: the down launch's last workgroup
+    combines and re-arms its counter, so every call must match the oracle.
+    512: the shared expert is a separate launch, which then combines."""
+    rng, router, gpu, cpu = _small_case(ctx, orc, 390 + shared_inter, shared_inter=shared_inter)
+    try:
+        for t, level in ((1, 0), (1, 0), (3, 0), (1, 3), (1, 0), (1, 1)):
+            h = rng.standard_normal((t, SMALL["H"])).astype(np.float32)
+            out_g, ids_g, w_g = gpu.ffn(h, level=level)
+            out_c, ids_c, w_c = cpu.ffn(h, level=level)
+            _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+    finally:
+        gpu.free()
+
+
 @pytest.mark.parametrize("level", [0, 1, 2, 3])
 @pytest.mark.parametrize("t", [1, 9])
 def test_throttle_levels(ctx, orc, level, t):
