@@ -80,7 +80,7 @@ __device__ __forceinline__ bool select_problem(const GemvArgs& a, uint32_t p, ui
     x_row = p;
     y_row = p;
     if constexpr (ROUTE) {
-        // Every wave routes the token (same result); the problem follows.
+        // Routes the token (run by one wave); the problem follows.
         const TokenRoute tr = route_token(a.route, 0);
         if (p == 0 && blockIdx.x == 0 && threadIdx.x == 0) decode_route_outputs(a.route, tr);
         const uint32_t E = a.route.n_experts;
@@ -169,6 +169,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
         uint8_t aq[kQChunkBlocks * 64];
         float xs[kQChunkBlocks];
         float row_sum[kQMaxTiles * 16];
+        uint32_t sel[2];  // ROUTE: the routed problem's matrix (~0u: none) and output row
     };
     __shared__ __align__(16) Lds lds;
     uint32_t* const tab = lds.tab;
@@ -181,8 +182,9 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // The problem: known up front, except in the decode gate/up variant,
-    // which routes the token after its table and activation loads (row 0)
-    // are issued, so the routing overlaps their latency.
+    // where wave 0 routes the token after every wave's table and activation
+    // loads (row 0) are issued, so the routing overlaps their latency (one
+    // wave: sixteen waves routing the same token cost ~2 us of issue time).
     uint64_t mat = 0, x_row = 0, y_row = 0;
     if constexpr (!ROUTE) {
         if (!select_problem<false>(a, blockIdx.y, mat, x_row, y_row)) return;  // whole workgroup
@@ -257,13 +259,27 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
         x_pass_load(x_r, 0, xv);
         x_pass_load(u_r, 0, uv);
         if constexpr (ROUTE) {
-            if (!select_problem<true>(a, blockIdx.y, mat, x_row, y_row)) return;  // whole workgroup; x_row stays 0
+            // Wave 0 routes the token and hands the problem to the others
+            // through LDS; the barrier also orders every wave's loads above
+            // before its weight loads.
+            if (wave == 0) {
+                const bool run = select_problem<true>(a, blockIdx.y, mat, x_row, y_row);
+                if (lane == 0) {
+                    lds.sel[0] = run ? (uint32_t)mat : ~0u;
+                    lds.sel[1] = (uint32_t)y_row;
+                }
+            }
+            lds_barrier();
+            const uint32_t sel = lds.sel[0];
+            if (sel == ~0u) return;  // whole workgroup; x_row stays 0
+            mat = sel;
+            y_row = lds.sel[1];
         }
         y_base = a.y + y_row * a.y_stride;
         rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
         d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
         start_chunk(0, uc0);
-        __builtin_amdgcn_s_barrier();
+        if constexpr (!ROUTE) __builtin_amdgcn_s_barrier();
         issue_first();
 #pragma unroll
         for (int i = 0; i < 2; ++i) reinterpret_cast<uint4*>(tab)[threadIdx.x + kQWg * i] = tv[i];

@@ -209,11 +209,65 @@ __device__ inline TokenRoute finish_route(const RouteArgs& a, const uint32_t (&i
     return r;
 }
 
+// Integer key of a float whose signed order is the float order (NaN aside):
+// negative values get their magnitude bits flipped. -0 and +0 get different
+// keys; callers detect equal floats by a float compare.
+__device__ __forceinline__ int order_key(float f) {
+    const int b = __float_as_int(f);
+    return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float key_float(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7FFFFFFF)); }
+
+// Wave-wide signed max, every lane receives it (the DPP steps of wave_max on
+// integers: no float canonicalisation between steps).
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
+    const auto p = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = max((int)p[0], (int)p[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return max((int)q[0], (int)q[1]);
+}
+
+// top_k_distinct for n <= 64 (score j in lane j): each of the k rounds
+// takes the largest remaining key and fails (heap fallback) unless exactly
+// one remaining score equals it as a float (which also catches -0 against
+// +0). When all k rounds succeed, the k picks are distinct and strictly
+// above every other score, so math.topK returns them in this order whatever
+// its insertion order. No live key is kKeyNone: only a NaN maps there.
+constexpr int kKeyNone = (int)0x80000000;
+__device__ inline bool top_k_distinct64(float v, uint32_t n, uint32_t k, uint32_t (&ids)[kMaxK],
+                                        float (&ts)[kMaxK]) {
+    const uint32_t lane = threadIdx.x & 63;
+    bool live = lane < n;
+    if (__any(live && v != v)) return false;
+    int key = live ? order_key(v) : kKeyNone;
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxK; ++r) {  // constant r: ids / ts stay in registers
+        if (r >= k) break;
+        const float m = key_float(wave_max_i32(key));
+        const unsigned long long who = __ballot(live && v == m);
+        if (__popcll(who) != 1) return false;
+        const uint32_t wl = (uint32_t)__builtin_ctzll(who);
+        ids[r] = wl;
+        ts[r] = m;
+        if (lane == wl) {
+            live = false;
+            key = kKeyNone;
+        }
+    }
+    return true;
+}
+
 // Routing of one token by a whole wave (scores one per lane).
 __device__ inline TokenRoute route_scores(const RouteArgs& a, const float (&sc)[4]) {
     uint32_t ids[kMaxK] = {0, 0, 0, 0};
     float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f};
-    if (!top_k_distinct(sc, a.n_experts, a.k, ids, ts)) top_k_wave(sc, a.n_experts, a.k, ids, ts);
+    const bool fast = a.n_experts <= 64 ? top_k_distinct64(sc[0], a.n_experts, a.k, ids, ts)
+                                        : top_k_distinct(sc, a.n_experts, a.k, ids, ts);
+    if (!fast) top_k_wave(sc, a.n_experts, a.k, ids, ts);
     return finish_route(a, ids, ts);
 }
 

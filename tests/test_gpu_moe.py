@@ -145,9 +145,10 @@ def test_token_counts(ctx, orc, t):
 @pytest.mark.parametrize("shared_inter", [256, 512])
 def test_decode_calls_in_a_row(ctx, orc, shared_inter):
     """Decode calls back to back on one layer, a prefill call and a heavy-throttle
-    call (one routed expert) in between: the down launch's last workgroup
-    combines and re-arms its counter, so every call must match the oracle.
-    512: the shared expert is a separate launch, which then combines."""
+    call (one routed expert) in between: the routing outputs and problem lists
+    the decode kernels leave in the layer's scratch are rewritten on every
+    call, so every call must match the oracle. 512: the shared expert runs as
+    separate launches."""
     rng, router, gpu, cpu = _small_case(ctx, orc, 390 + shared_inter, shared_inter=shared_inter)
     try:
         for t, level in ((1, 0), (1, 0), (3, 0), (1, 3), (1, 0), (1, 1)):
@@ -261,6 +262,42 @@ def test_invalid_calls(ctx, orc):
             gpu.ffn(np.zeros((257, SMALL["H"]), np.float32))
     finally:
         gpu.free()
+
+
+@pytest.mark.parametrize("level", [0, 2, 3])
+def test_decode_routing_ties_follow_the_heap(ctx, orc, level):
+    """Decode calls (one token each, routed inside the gate/up kernel) under an
+    identity router: four-valued scores that tie at the k-th place, a token
+    whose two largest scores are +0 and -0 (equal as floats, so the heap's
+    insertion order decides), a NaN score past the heap's seed positions, and
+    distinct scores. Ids and their order must be math.topK's
+    (math.zig:130-174)."""
+    rng = np.random.default_rng(420 + level)
+    H, I, E = 512, 256, 64
+    _, gate, up, down, shared = _weights(rng, mm.IQ2_XXS, H, I, E, shared_inter=I)
+    router = np.zeros((E, H), dtype=np.float32)
+    router[:, :E] = np.eye(E, dtype=np.float32)
+    rows = [rng.choice(np.array([-1.0, 0.0, 0.5, 1.0], dtype=np.float32), E) for _ in range(10)]
+    zeros = (-1.0 - rng.random(E)).astype(np.float32)
+    zeros[[9, 3]] = np.array([-0.0, 0.0], dtype=np.float32)
+    rows += [zeros, zeros[::-1].copy(), rng.standard_normal(E).astype(np.float32)]
+    # Expert 37's router row also reads a column past the identity block with
+    # a NaN weight: only its score is NaN.
+    nan_router = router.copy()
+    nan_router[37, E + 5] = np.nan
+    for rt, rr in ((router, rows), (nan_router, rows[:2] + rows[-1:])):
+        gpu, cpu = _layers(ctx, orc, mm.IQ2_XXS, H, I, E, rt, gate, up, down, shared, shared_inter=I)
+        try:
+            for r in rr:
+                h = rng.standard_normal((1, H)).astype(np.float32)
+                h[0, :E] = r
+                out_g, ids_g, w_g = gpu.ffn(h, level=level)
+                out_c, ids_c, w_c = cpu.ffn(h, level=level)
+                np.testing.assert_array_equal(ids_g, ids_c)
+                np.testing.assert_allclose(w_g, w_c, rtol=TOL_W, atol=1e-7)
+                assert mm.max_abs_rel(out_g, out_c) < TOL_OUT
+        finally:
+            gpu.free()
 
 
 @pytest.mark.parametrize("level", [0, 1, 2, 3])
