@@ -47,7 +47,6 @@ struct GroupArgs {
     uint64_t mat;                   // dense: matrix
     uint32_t batch;                 // dense: rows of the batch
     uint32_t tiles, units, rows;
-    uint32_t tiles_per_wg;
 };
 
 // LDS A layout of one chunk: block pair p (blocks 2p, 2p+1) is 1 KiB; lane
@@ -132,35 +131,33 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
     __shared__ __align__(16) uint8_t aq[kGChunkBlocks * 512];
     __shared__ __align__(16) float xs_lds[kGRows * kGChunkBlocks];
 
-    // Item: matrix, first slot, rows.
-    uint64_t mat = a.mat;
-    uint32_t first = blockIdx.y * kGRows, count = 0, col_off = 0;
-    if (a.work) {
-        if (blockIdx.y >= *a.n_work) return;  // whole workgroup
-        const QmmWork w = a.work[blockIdx.y];
-        mat = w.mat;
-        first = w.slot;
-        count = w.count;
-        col_off = w.pad;
-    } else {
-        count = a.batch > first ? min(a.batch - first, kGRows) : 0;
-    }
+    // This workgroup's share of the (item, row tile) pairs, item-major:
+    // equal contiguous ranges over the grid, so every workgroup streams the
+    // same number of tiles whatever number of items the routing produced
+    // (the host sizes the grid before the routing runs). A range covers whole
+    // or partial tile runs of one or two items; the activations are staged
+    // once per item run.
+    const uint32_t n_items = a.work ? *a.n_work : (a.batch + kGRows - 1) / kGRows;
+    const uint64_t total = (uint64_t)n_items * a.tiles;
+    uint64_t q = total * blockIdx.x / gridDim.x;
+    const uint64_t q_end = total * (blockIdx.x + 1) / gridDim.x;
+    if (q >= q_end) return;  // whole workgroup
+
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nblk_all = a.units * kBlkPerUnit;
     const uint32_t chunk_blk = nblk_all < kGChunkBlocks ? nblk_all : kGChunkBlocks;
     const uint32_t chunk_units = chunk_blk / kBlkPerUnit;
-    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
-    uint32_t my_n = 0;
-    if (t_begin + wave < a.tiles) {
-        const uint32_t t_end = min(a.tiles, t_begin + a.tiles_per_wg);
-        my_n = (t_end - (t_begin + wave) + kWaves - 1) / kWaves;
-    }
-    const BufRsrc rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
-    const BufRsrc d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
     const uint32_t rec_voff = lane * 16;
     const uint32_t d_voff = n * a.d_row * 2;
+
+    // Current item run: matrix, first slot, rows, output column offset, and
+    // tiles [t_begin, t_begin + run) split over the waves (wave v: t_begin +
+    // v + kWaves i).
+    uint64_t mat = a.mat;
+    uint32_t first = 0, count = 0, col_off = 0, t_begin = 0, my_n = 0;
+    BufRsrc rec_r, d_r;
     // Activation row of item row j (rows past `count` repeat row 0: their
     // results are computed and dropped).
     auto act_row = [&](uint32_t j) -> uint64_t {
@@ -169,10 +166,9 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
     };
 
     uint32_t u_begin = 0;
-    uint32_t n_sub = min(a.units, chunk_units) / UPS;
+    uint32_t n_sub = 1, steps = 0;
     auto tile_of = [&](uint32_t s) { return t_begin + wave + kWaves * (s / n_sub); };
     auto first_unit = [&](uint32_t s) { return u_begin + (s % n_sub) * UPS; };
-    uint32_t steps = my_n * n_sub;
     uint4 r0[kMaxUnitsPerStep], r1[kMaxUnitsPerStep], r2[kMaxUnitsPerStep];
     uint32_t d0[kMaxUnitsPerStep], d1[kMaxUnitsPerStep], d2[kMaxUnitsPerStep];
     auto load = [&](uint32_t s, uint4 (&r)[kMaxUnitsPerStep], uint32_t (&dw)[kMaxUnitsPerStep]) {
@@ -243,6 +239,32 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
             if (e % kGChunkBlocks < nb) xs_lds[e] = sc[i];
         }
     };
+
+    // Takes the next run of the range: its item and tiles.
+    auto next_run = [&]() {
+        const uint32_t item = (uint32_t)(q / a.tiles);
+        t_begin = (uint32_t)(q % a.tiles);
+        const uint32_t run = (uint32_t)min((uint64_t)(a.tiles - t_begin), q_end - q);
+        q += run;
+        if (a.work) {
+            const QmmWork w = a.work[item];
+            mat = w.mat;
+            first = w.slot;
+            count = w.count;
+            col_off = w.pad;
+        } else {
+            first = item * kGRows;
+            count = min(a.batch - first, kGRows);
+        }
+        my_n = wave < run ? (run - wave + kWaves - 1) / kWaves : 0;
+        rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
+        d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
+        u_begin = 0;
+        n_sub = min(a.units, chunk_units) / UPS;
+        steps = my_n * n_sub;
+        kb = 0;
+    };
+    next_run();
     {
         // Small loads first and waited for: a CU returns loads in issue order
         // across its waves, so weights issued first would hold them back.
@@ -269,15 +291,23 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
             load(s + 5, r2, d2);
         }
         kb += chunk_blk;
-        if (kb >= nblk_all) break;
-        const uint32_t nb = min(chunk_blk, nblk_all - kb);
-        lds_barrier();  // previous chunk's LDS no longer in use
-        u_begin = kb / kBlkPerUnit;
-        n_sub = (nb / kBlkPerUnit) / UPS;
-        steps = my_n * n_sub;
+        uint32_t kb0 = kb, nb = chunk_blk;
+        if (kb < nblk_all) {
+            // Next K-chunk of this run.
+            nb = min(chunk_blk, nblk_all - kb);
+            u_begin = kb / kBlkPerUnit;
+            n_sub = (nb / kBlkPerUnit) / UPS;
+            steps = my_n * n_sub;
+        } else {
+            if (q >= q_end) break;
+            next_run();  // the next item's run, from its first chunk
+            kb0 = 0;
+        }
+        lds_barrier();  // the previous chunk's LDS no longer in use
         uint2 lo[kPer], hi[kPer];
         float sc[2];
-        stage_load(kb, nb, lo, hi, sc);
+        stage_load(kb0, nb, lo, hi, sc);
+        if (kb0 == 0) vm_wait_all();  // a new item: small loads ahead of its weights
         load(0, r0, d0);
         load(1, r1, d1);
         load(2, r2, d2);
@@ -328,13 +358,14 @@ hipError_t launch(GroupArgs a, uint32_t fmt, uint32_t items, int num_cu, hipStre
     const int ups = group_ups(fmt, a.units);
     const void* fn = fmt == kFmtIq2 ? (wg == 512 ? group_kernel_for<kFmtIq2, 512>(ups) : group_kernel_for<kFmtIq2, 256>(ups))
                                     : (wg == 512 ? group_kernel_for<kFmtQ8, 512>(ups) : group_kernel_for<kFmtQ8, 256>(ups));
+    // Every resident workgroup slot of the device, or fewer when the largest
+    // possible call has under one tile per wave for each of them; each
+    // workgroup takes 1 / grid of the items' tiles (the actual item count
+    // of a grouped call is only known on the device).
     const uint32_t waves = wg / 64;
-    const uint64_t target = (uint64_t)(num_cu > 0 ? num_cu : 256) * resident(fn, wg);
-    uint64_t tpw = ((uint64_t)items * a.tiles + target - 1) / target;
-    tpw = (tpw + waves - 1) / waves * waves;
-    if (tpw > a.tiles) tpw = (a.tiles + waves - 1) / waves * waves;
-    a.tiles_per_wg = (uint32_t)tpw;
-    const dim3 grid((unsigned)((a.tiles + tpw - 1) / tpw), items);
+    const uint64_t slots = (uint64_t)(num_cu > 0 ? num_cu : 256) * resident(fn, wg);
+    const uint64_t most = ((uint64_t)items * a.tiles + waves - 1) / waves;
+    const dim3 grid((unsigned)(most < slots ? most : slots));
     void* args[] = {&a};
     return hipLaunchKernel(fn, grid, dim3(wg), args, 0, s);
 }

@@ -57,7 +57,7 @@ __device__ void route_body(const RouteArgs& a, RouteLds& L) {
     // first lane writes the token's results.
     for (uint32_t t0 = 4 * wave; t0 < T; t0 += 4 * (kRouteThreads / 64)) {
         const uint32_t t = t0 + (lane >> 4);
-        const TokenRoute tr = route_row16(a, t);
+        const TokenRoute tr = E <= 64 ? route_row16<4>(a, t) : route_row16<16>(a, t);
         if ((lane & 15) == 0 && t < T) {
             const uint32_t act = tr.act;
 #pragma unroll

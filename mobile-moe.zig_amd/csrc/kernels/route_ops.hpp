@@ -272,18 +272,13 @@ __device__ inline TokenRoute route_scores(const RouteArgs& a, const float (&sc)[
 }
 
 // Routing of 4 tokens per wave, one per 16-lane row: lane p of a row holds
-// the token's scores p, p + 16, ..., p + 240 (experts past n_experts are
-// never selected). k + 1 rounds of a row-wide max pick the selected experts
-// as top_k_distinct does, all rows at once; a row whose k + 1 largest scores
-// are not distinct, or that holds a NaN, is routed by math.topK's heap over
-// the token's scores in memory instead (exact insertion order), by the row's
-// first lane. t is the row's token; rows with t >= n_tokens do nothing useful.
-__device__ __forceinline__ float row_max16(float v) {
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
-    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
-}
+// the token's scores p, p + 16, ... (experts past n_experts are never
+// selected). k rounds of a row-wide max pick the selected experts as
+// top_k_distinct64 does, all rows at once; a row whose k largest scores are
+// not distinct and strictly above the rest, or that holds a NaN, is routed
+// by math.topK's heap over the token's scores in memory instead (exact
+// insertion order), by the row's first lane. t is the row's token; rows with
+// t >= n_tokens do nothing useful.
 __device__ __forceinline__ uint32_t row_max16u(uint32_t v) {
     v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
     v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
@@ -291,52 +286,59 @@ __device__ __forceinline__ uint32_t row_max16u(uint32_t v) {
     return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
 }
 
+__device__ __forceinline__ int row_max16i(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
+    return max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
+}
+
+// NC score slots per lane: lane p of a row holds experts p + 16 c, c < NC
+// (NC = 4 covers 64 experts, 16 covers 256). Each of the k rounds takes the
+// row's largest remaining key (order_key) and is clean when exactly one live
+// score of the row equals it as a float; the k picks of clean rounds are
+// distinct and above every other score, which is math.topK's result.
+template <int NC>
 __device__ inline TokenRoute route_row16(const RouteArgs& a, uint32_t t) {
     const uint32_t lane = threadIdx.x & 63, p = lane & 15, row = lane >> 4;
     const uint32_t E = a.n_experts, k = a.k;
     const bool live = t < a.n_tokens;
     const BufRsrc sr = make_rsrc(a.scores + (uint64_t)(live ? t : 0) * E, live ? E * 4 : 0);
-    float sc[16];
+    float sc[NC];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) sc[c] = __uint_as_float(buf_load_b32(sr, (p + 16 * c) * 4, 0));
-    uint32_t valid = 0;
+    for (int c = 0; c < NC; ++c) sc[c] = __uint_as_float(buf_load_b32(sr, (p + 16 * c) * 4, 0));
+    int key[NC];
     bool bad = false;
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
-        if (p + 16 * c < E) {
-            valid |= 1u << c;
-            bad |= sc[c] != sc[c];
-        }
+    for (int c = 0; c < NC; ++c) {
+        const bool v = p + 16 * c < E;
+        bad |= v && sc[c] != sc[c];
+        key[c] = v ? order_key(sc[c]) : kKeyNone;
+    }
     uint32_t ids[kMaxK] = {0, 0, 0, 0};
     float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f};
-    const uint32_t rounds = k < E ? k + 1 : k;
 #pragma unroll
-    for (uint32_t r = 0; r < kMaxK + 1; ++r) {  // constant r: ids / ts stay in registers
-        if (r >= rounds) break;
-        float best = -__builtin_inff();
-        uint32_t bc = 16, dup = 0;
+    for (uint32_t r = 0; r < kMaxK; ++r) {  // constant r: ids / ts stay in registers
+        if (r >= k) break;
+        int lk = key[0];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            if (!((valid >> c) & 1u)) continue;
-            if (bc == 16 || sc[c] > best) {
-                best = sc[c];
-                bc = c;
-                dup = 0;
-            } else if (sc[c] == best) {
-                dup = 1;
+        for (int c = 1; c < NC; ++c) lk = max(lk, key[c]);
+        const float m = key_float(row_max16i(lk));
+        uint32_t hits = 0, hc = 0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (key[c] != kKeyNone && sc[c] == m) {
+                ++hits;
+                hc = c;
             }
-        }
-        const float m = row_max16(bc < 16 ? best : -__builtin_inff());
-        const bool mine = bc < 16 && best == m;
-        const unsigned long long who = __ballot(mine);
+        const unsigned long long who = __ballot(hits != 0);
         const uint32_t in_row = (uint32_t)(who >> (16 * row)) & 0xFFFFu;
-        if (__builtin_popcount(in_row) != 1 || (mine && dup)) bad = true;
-        const uint32_t id = row_max16u(mine ? p + 16 * bc + 1 : 0u) - 1u;
-        if (r < k) {
-            ids[r] = id;
-            ts[r] = m;
-        }
-        if (mine) valid &= ~(1u << bc);
+        if (__builtin_popcount(in_row) != 1 || hits > 1) bad = true;
+        ids[r] = row_max16u(hits ? p + 16 * hc + 1 : 0u) - 1u;
+        ts[r] = m;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (hits && hc == (uint32_t)c) key[c] = kKeyNone;
     }
     // A row is bad when any of its lanes saw a clash.
     const unsigned long long bad_rows = __ballot(bad);

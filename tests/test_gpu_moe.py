@@ -264,6 +264,38 @@ def test_invalid_calls(ctx, orc):
         gpu.free()
 
 
+@pytest.mark.parametrize("n_exp", [128, 256])
+@pytest.mark.parametrize("t", [1, 24])
+def test_many_experts(ctx, orc, n_exp, t):
+    """More than 64 experts (up to the 256 the routing kernels hold), decode and
+    grouped prefill, with distinct router logits and then with identity-router
+    scores from four values (ties at the k-th place, heap order)."""
+    rng = np.random.default_rng(450 + n_exp + t)
+    H, I = 256, 256
+    router, gate, up, down, shared = _weights(rng, mm.IQ2_XXS, H, I, n_exp, shared_inter=I, router_sigma=0.05)
+    gpu, cpu = _layers(ctx, orc, mm.IQ2_XXS, H, I, n_exp, router, gate, up, down, shared, shared_inter=I)
+    try:
+        h = rng.standard_normal((t, H)).astype(np.float32)
+        out_g, ids_g, w_g = gpu.ffn(h)
+        out_c, ids_c, w_c = cpu.ffn(h)
+        _check(orc, router, h, out_g, ids_g, w_g, out_c, ids_c, w_c)
+    finally:
+        gpu.free()
+    ident = np.zeros((n_exp, H), dtype=np.float32)
+    ident[:, :n_exp] = np.eye(n_exp, dtype=np.float32)
+    gpu, cpu = _layers(ctx, orc, mm.IQ2_XXS, H, I, n_exp, ident, gate, up, down, shared, shared_inter=I)
+    try:
+        h = rng.standard_normal((t, H)).astype(np.float32)
+        h[:, :n_exp] = rng.choice(np.array([-1.0, 0.0, 0.5, 1.0], dtype=np.float32), (t, n_exp))
+        out_g, ids_g, w_g = gpu.ffn(h)
+        out_c, ids_c, w_c = cpu.ffn(h)
+        np.testing.assert_array_equal(ids_g, ids_c)
+        np.testing.assert_allclose(w_g, w_c, rtol=TOL_W, atol=1e-7)
+        assert mm.max_abs_rel(out_g, out_c) < TOL_OUT
+    finally:
+        gpu.free()
+
+
 @pytest.mark.parametrize("level", [0, 2, 3])
 def test_decode_routing_ties_follow_the_heap(ctx, orc, level):
     """Decode calls (one token each, routed inside the gate/up kernel) under an
