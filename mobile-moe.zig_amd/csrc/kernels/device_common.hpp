@@ -47,6 +47,7 @@
 namespace mmhip {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 constexpr int kTileRows = 16;

@@ -253,47 +253,83 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     }
 }
 
-// f32 / f16 weights: one 256-thread workgroup per output row. Each pass
-// covers 2048 columns (8 per thread) with all of a thread's loads in flight
-// together; out-of-range columns read as zero through the buffer resources.
+// f32 / f16 weights: one 256-thread workgroup per output row and NT
+// vectors (NT > 1 only when all vectors share one matrix, as a batch of
+// tokens shares the router): the row's columns are loaded once and used for
+// every vector. Each pass covers 2048 columns (8 per thread) with all of a
+// thread's loads in flight together; out-of-range columns, and vectors past
+// n_mats, read as zero through the buffer resources. A vector's sum runs in
+// the same order whatever NT is, so a token's scores do not depend on the
+// batch it came in.
 constexpr int kFloatThreads = 256;
-template <typename WT>
+// Four f32 at element e (4-aligned when vec).
+__device__ __forceinline__ void load4(BufRsrc r, uint32_t e, bool vec, float* out) {
+    if (vec) {
+        const uint4 v = buf_load_b128(r, e * 4, 0);
+        out[0] = __uint_as_float(v.x);
+        out[1] = __uint_as_float(v.y);
+        out[2] = __uint_as_float(v.z);
+        out[3] = __uint_as_float(v.w);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(buf_load_b32(r, (e + i) * 4, 0));
+    }
+}
+template <typename WT, int NT>
 __global__ __launch_bounds__(kFloatThreads) void gemv_float_kernel(const WT* __restrict__ w, uint64_t mat_stride,
                                                                    const float* __restrict__ x, uint64_t x_stride,
                                                                    float* __restrict__ y, uint64_t y_stride,
-                                                                   uint32_t rows, uint32_t cols) {
-    __shared__ float part[kFloatThreads / 64];
-    const uint32_t m = blockIdx.y, r = blockIdx.x;
-    const BufRsrc wr = make_rsrc(w + m * mat_stride + (uint64_t)r * cols, cols * (uint32_t)sizeof(WT));
-    const BufRsrc xr = make_rsrc(x + m * x_stride, cols * 4);
-    float acc = 0.0f;
+                                                                   uint32_t n_mats, uint32_t rows, uint32_t cols) {
+    __shared__ float part[NT][kFloatThreads / 64];
+    const uint32_t m0 = blockIdx.y * NT, r = blockIdx.x;
+    const bool vec = cols % 4 == 0;  // 16-byte loads; otherwise one load per column (per-column bounds)
+    const BufRsrc wr = make_rsrc(w + m0 * mat_stride + (uint64_t)r * cols, cols * (uint32_t)sizeof(WT));
+    float acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = 0.0f;
     for (uint32_t c0 = 0; c0 < cols; c0 += kFloatThreads * 8) {
         const uint32_t c = c0 + threadIdx.x * 4;
-        float wv[8], xv[8];
+        float wv[8];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t cc = c + h * kFloatThreads * 4;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) xv[4 * h + e] = __uint_as_float(buf_load_b32(xr, (cc + e) * 4, 0));
             if constexpr (sizeof(WT) == 2) {
+                if (vec) {
+                    const uint2 hv = buf_load_b64(wr, cc * 2, 0);
+                    wv[4 * h + 0] = f16_bits_to_f32(hv.x & 0xFFFFu);
+                    wv[4 * h + 1] = f16_bits_to_f32(hv.x >> 16);
+                    wv[4 * h + 2] = f16_bits_to_f32(hv.y & 0xFFFFu);
+                    wv[4 * h + 3] = f16_bits_to_f32(hv.y >> 16);
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) wv[4 * h + e] = f16_bits_to_f32(buf_load_b16(wr, (cc + e) * 2, 0));
+                    for (int e = 0; e < 4; ++e) wv[4 * h + e] = f16_bits_to_f32(buf_load_b16(wr, (cc + e) * 2, 0));
+                }
             } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) wv[4 * h + e] = __uint_as_float(buf_load_b32(wr, (cc + e) * 4, 0));
+                load4(wr, cc, vec, wv + 4 * h);
             }
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc = fmaf(wv[e], xv[e], acc);
+        for (int j = 0; j < NT; ++j) {
+            const uint32_t m = m0 + j;
+            const BufRsrc xr = make_rsrc(x + (uint64_t)(m < n_mats ? m : 0) * x_stride, m < n_mats ? cols * 4 : 0);
+            float xv[8];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) load4(xr, c + h * kFloatThreads * 4, vec, xv + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[j] = fmaf(wv[e], xv[e], acc[j]);
+        }
     }
-    acc = wave_sum(acc);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const float v = wave_sum(acc[j]);
+        if ((threadIdx.x & 63) == 0) part[j][threadIdx.x >> 6] = v;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < NT && m0 + threadIdx.x < n_mats) {
         float t = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kFloatThreads / 64; ++i) t += part[i];
-        y[m * y_stride + r] = t;
+        for (int i = 0; i < kFloatThreads / 64; ++i) t += part[threadIdx.x][i];
+        y[(m0 + threadIdx.x) * y_stride + r] = t;
     }
 }
 
@@ -384,13 +420,24 @@ hipError_t launch_gemv_float(const void* w, uint32_t type, uint64_t mat_stride, 
                              uint64_t x_stride, float* y, uint64_t y_stride, uint32_t n_mats,
                              uint32_t rows, uint32_t cols, hipStream_t s) {
     if ((uint64_t)n_mats * rows == 0) return hipSuccess;
+    if (mat_stride == 0 && n_mats > 1) {
+        // One matrix, several vectors: 16 vectors per workgroup.
+        const dim3 grid(rows, (n_mats + 15) / 16);
+        if (type == 0)
+            gemv_float_kernel<float, 16><<<grid, kFloatThreads, 0, s>>>((const float*)w, 0, x, x_stride, y, y_stride,
+                                                                        n_mats, rows, cols);
+        else
+            gemv_float_kernel<uint16_t, 16><<<grid, kFloatThreads, 0, s>>>((const uint16_t*)w, 0, x, x_stride, y,
+                                                                           y_stride, n_mats, rows, cols);
+        return hipGetLastError();
+    }
     const dim3 grid(rows, n_mats);
     if (type == 0)
-        gemv_float_kernel<float><<<grid, kFloatThreads, 0, s>>>((const float*)w, mat_stride, x, x_stride, y, y_stride,
-                                                               rows, cols);
+        gemv_float_kernel<float, 1><<<grid, kFloatThreads, 0, s>>>((const float*)w, mat_stride, x, x_stride, y,
+                                                                   y_stride, n_mats, rows, cols);
     else
-        gemv_float_kernel<uint16_t><<<grid, kFloatThreads, 0, s>>>((const uint16_t*)w, mat_stride, x, x_stride, y,
-                                                                  y_stride, rows, cols);
+        gemv_float_kernel<uint16_t, 1><<<grid, kFloatThreads, 0, s>>>((const uint16_t*)w, mat_stride, x, x_stride, y,
+                                                                      y_stride, n_mats, rows, cols);
     return hipGetLastError();
 }
 

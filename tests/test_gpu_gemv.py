@@ -152,6 +152,22 @@ def test_qmm_batch64_config(ctx, orc, t, rows, cols):
     assert err <= TOL_GEMV   # the int8-digit MFMA path also meets the f32 bar
 
 
+@pytest.mark.parametrize("t", [mm.F32, mm.F16])
+@pytest.mark.parametrize("batch,rows,cols", [(5, 80, 320), (16, 64, 2048), (37, 200, 1024), (64, 64, 2048),
+                                             (9, 48, 330)])
+def test_float_weights_batched(ctx, orc, t, batch, rows, cols):
+    """f32 / f16 weights times a batch (the router of a prefill call): batches
+    above 4 with columns a multiple of 4 run as 16 x 16 f32 MFMA tiles; rows
+    and batches that are not multiples of 16 leave partial tiles; 330 columns
+    take the one-row-per-workgroup kernel. f32 accumulation: TOL_GEMV."""
+    rng = np.random.default_rng(batch * 7 + rows + t)
+    raw = _weights(rng, t, rows, cols)
+    xin = rng.standard_normal((batch, cols)).astype(np.float32)
+    ref = orc.batch_mat_mul_unified(raw, t, xin, rows, batch, cols)
+    got = ctx.batch_mat_mul(raw, t, xin, rows, batch, cols)
+    assert mm.max_abs_rel(got, ref) <= TOL_GEMV
+
+
 @pytest.mark.parametrize("batch", [1, 2, 7, 33, 100])
 def test_qmm_ragged_batches_and_layouts(ctx, orc, batch):
     rng = np.random.default_rng(batch)
