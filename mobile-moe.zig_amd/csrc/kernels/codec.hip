@@ -190,25 +190,10 @@ __global__ __launch_bounds__(256) void quantize_wide_kernel(const float* __restr
                                                              uint64_t s_stride) {
     const uint32_t nunit = cols_pad / 256;
     const uint64_t unit = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const uint32_t lane = threadIdx.x & 63;
     const uint32_t rows = n_rows ? min(*n_rows, n_max) : n_max;
     if (unit >= (uint64_t)rows * nunit) return;  // whole wave exits together
-    const uint64_t v = unit / nunit;
-    const uint32_t u = (uint32_t)(unit % nunit);
-    const uint32_t c0 = u * 256 + lane * 4;
-    const float* g = src + v * src_stride;
-    float x[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint32_t col = c0 + e;
-        x[e] = 0.0f;
-        if (col < cols) x[e] = SILU ? silu(g[col]) * g[u_off + col] : g[col];
-    }
-    uint32_t h4, l4;
-    const float s = quantize_quad_wave(x, h4, l4);
-    *reinterpret_cast<uint32_t*>(hi + v * q_stride + c0) = h4;
-    *reinterpret_cast<uint32_t*>(lo + v * q_stride + c0) = l4;
-    if (lane < 8) sc[v * s_stride + u * 8 + lane] = s;
+    quantize_unit_wave<SILU>(src, src_stride, u_off, unit / nunit, (uint32_t)(unit % nunit), cols, hi, lo, sc, q_stride,
+                             s_stride);
 }
 
 }  // namespace

@@ -408,6 +408,32 @@ __device__ __forceinline__ void x_pass_load(BufRsrc xr, uint32_t b0, float (&v)[
 // silu(x) = x / (1 + exp(-x))  (math.zig:38-41).
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
+// Wide activation quantisation by one wave: unit u (256 columns, 4 per lane)
+// of vector v of src (silu(g) * g[u_off + col] when SILU) into the digit
+// planes, its scale stored in the unit's eight block slots.
+template <bool SILU>
+__device__ __forceinline__ void quantize_unit_wave(const float* __restrict__ src, uint64_t src_stride, uint64_t u_off,
+                                                   uint64_t v, uint32_t u, uint32_t cols, int8_t* __restrict__ hi,
+                                                   int8_t* __restrict__ lo, float* __restrict__ sc, uint64_t q_stride,
+                                                   uint64_t s_stride) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t c0 = u * 256 + lane * 4;
+    const float* g = src + v * src_stride;
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t col = c0 + e;
+        x[e] = 0.0f;
+        if (col < cols) x[e] = SILU ? silu(g[col]) * g[u_off + col] : g[col];
+    }
+    uint32_t h4, l4;
+    const float s = quantize_quad_wave(x, h4, l4);
+    *reinterpret_cast<uint32_t*>(hi + v * q_stride + c0) = h4;
+    *reinterpret_cast<uint32_t*>(lo + v * q_stride + c0) = l4;
+    if (lane < 8) sc[v * s_stride + u * 8 + lane] = s;
+}
+
+
 // v = silu(v) * u elementwise (expertFFN's siluInplace + mul, inference.zig:1179-1180).
 __device__ __forceinline__ void silu_mul4(float (&v)[4], const float (&u)[4]) {
 #pragma unroll

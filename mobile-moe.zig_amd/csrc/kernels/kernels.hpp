@@ -62,6 +62,13 @@ struct RouteArgs {
     QmmWork* work_dn;
     uint32_t* n_work;           // [2]: active items of work_gu, work_dn
     uint32_t inter;             // routed expert width (up column offset)
+    // Optional, n_tokens > 1: the hidden states' wide quantisation (one
+    // scale per 256 columns) for the grouped gate/up, done by extra
+    // workgroups of the routing launch (it does not depend on the routing).
+    const float* qx = nullptr;  // [n_tokens][qx_stride]; null: no quantisation
+    uint64_t qx_stride = 0;
+    uint32_t q_cols = 0, q_units = 0;  // columns, 256-column units (cols_pad / 256)
+    QuantAct qa{};
 };
 
 struct GemvArgs {

@@ -1,6 +1,8 @@
 // MoE routing and combine on gfx950 (moeFFN, inference.zig:886-1010).
 //
-// route_kernel: one workgroup, four tokens per wave (one per 16-lane row). Each token runs
+// route_kernel: workgroup 0 routes, four tokens per wave (one per 16-lane
+// row); any further workgroups quantise the hidden states for the grouped
+// gate/up meanwhile (one wave per token and 256-column unit). Each token runs
 // Scheduler.route exactly as the CPU path does (math.topK's size-k min-heap,
 // softmax over the selected logits, throttle scaling, the heavy-throttle
 // top-1 fallback) and counts its experts (ExpertStats.counts). The workgroup
@@ -180,6 +182,14 @@ __device__ void route_body(const RouteArgs& a, RouteLds& L) {
 
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
     __shared__ RouteLds L;
+    if (blockIdx.x > 0) {
+        // Hidden-state quantisation: one wave per (token, 256-column unit).
+        const uint64_t unit = (uint64_t)(blockIdx.x - 1) * (kRouteThreads / 64) + (threadIdx.x >> 6);
+        if (unit < (uint64_t)a.n_tokens * a.q_units)
+            quantize_unit_wave<false>(a.qx, a.qx_stride, 0, unit / a.q_units, (uint32_t)(unit % a.q_units), a.q_cols,
+                                      a.qa.hi, a.qa.lo, a.qa.scale, a.qa.stride, a.qa.scale_stride);
+        return;
+    }
     route_body(a, L);
 }
 
@@ -216,7 +226,9 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t s) {
     if (a.n_tokens == 0 || a.n_tokens > kMaxTokens || a.n_experts > kMaxExperts || a.k == 0 || a.k > kMaxK ||
         a.k > a.n_experts)
         return hipErrorInvalidValue;
-    route_kernel<<<1, kRouteThreads, 0, s>>>(a);
+    const uint64_t q_waves = a.qx ? (uint64_t)a.n_tokens * a.q_units : 0;
+    const unsigned q_wgs = (unsigned)((q_waves + kRouteThreads / 64 - 1) / (kRouteThreads / 64));
+    route_kernel<<<1 + q_wgs, kRouteThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -14,7 +14,8 @@
 //     down          quantised GEMV, input silu(gate) * up
 //                   formed while quantising                  "moe_down"
 //   T > 1 (prefill, experts grouped):
-//     quantise hidden                                         "moe_quantize"
+//     quantise hidden (with IQ2_XXS experts: inside the
+//     routing launch)                                         "moe_quantize"
 //     gate/up       grouped QMM over expert-sorted slots      "moe_gateup"
 //     silu*up       quantised per slot                        "moe_quantize"
 //     down          grouped QMM                               "moe_down"
@@ -218,12 +219,24 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
         MOE_TRY(check_hip(launch_gemv_float(L->router->plain, L->router_type, 0, hidden, H, L->scores, E, T, E, H, s),
                           "moe: router"));
     }
+    const bool sep_shared = L->has_shared && !L->shared_merged;
+    const uint32_t SI = L->shared_inter;
+    // One activation scale per 256 columns when an IQ2_XXS grouped matmul
+    // reads the hidden digits (routed experts or the shared expert); then the
+    // routing launch also quantises them.
+    const bool wide_h = L->gu->geom.fmt == kFmtIq2 || (sep_shared && L->sh_gu->geom.fmt == kFmtIq2);
+    const QuantAct qh = quant_act_view(L->xq_h, T, L->gu->geom.cols_pad);
     if (T > 1) {
+        if (wide_h) {
+            r.qx = hidden;
+            r.qx_stride = H;
+            r.q_cols = H;
+            r.q_units = (uint32_t)(L->gu->geom.cols_pad / 256);
+            r.qa = qh;
+        }
         TimedLaunch tl(ctx, "moe_route");
         MOE_TRY(check_hip(launch_route(r, s), "moe: route"));
     }
-    const bool sep_shared = L->has_shared && !L->shared_merged;
-    const uint32_t SI = L->shared_inter;
     if (T == 1) {
         // Decode: the gate/up GEMV routes the token itself (no routing launch).
         MOE_TRY(gemv_launch(ctx, L->gu, "moe_gateup", nullptr, nullptr, L->shared_merged ? 10 : 8, hidden, 0, 0, false,
@@ -238,13 +251,9 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
     } else {
         const TileGeom& gg = L->gu->geom;
         const TileGeom& gd = L->dn->geom;
-        const QuantAct qh = quant_act_view(L->xq_h, T, gg.cols_pad);
-        {
+        if (!wide_h) {
             TimedLaunch tl(ctx, "moe_quantize");
-            // One activation scale per 256 columns when an IQ2_XXS grouped
-            // matmul reads the digits (routed experts or the shared expert).
-            const bool wide = gg.fmt == kFmtIq2 || (sep_shared && L->sh_gu->geom.fmt == kFmtIq2);
-            MOE_TRY(check_hip(launch_quantize(hidden, H, T, H, (uint32_t)gg.cols_pad, qh, s, wide), "moe: quantize"));
+            MOE_TRY(check_hip(launch_quantize(hidden, H, T, H, (uint32_t)gg.cols_pad, qh, s, false), "moe: quantize"));
         }
         {
             TimedLaunch tl(ctx, "moe_gateup");
