@@ -93,6 +93,9 @@ __device__ __forceinline__ void step_group_iq2(const uint4 (&r)[kMaxUnitsPerStep
             l0 = __mul24(dv[1], t) + l0;
             h1 = __mul24(dv[2], t) + h1;
             l1 = __mul24(dv[3], t) + l1;
+            // Keeps each sum a chain of 24-bit multiply-adds (one
+            // instruction per product) instead of products plus add trees.
+            asm("" : "+v"(h0), "+v"(l0), "+v"(h1), "+v"(l1));
         }
         const float c = f16_scale(iq2_scale_bits<UPS>(dw, i)) * 0.125f;
         acc0 = fmaf(fmaf((float)h0, 256.0f, (float)l0), c * x0, acc0);
