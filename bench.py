@@ -212,6 +212,51 @@ def moe_section(ctx, ev, rng, calls, n_layers=8, n_tokens=61):
     return out, warm, touched, (router, gate, up, down, shared, h64, id_router)
 
 
+def kv_codec_section(ctx, ev, rng, reps=20, n_rows=131072, row_len=576):
+    """Q8_0 KV-cache codec (KVCache.put / getKVCompressed's Q8_0 branches,
+    kv_cache.zig:225-349): n_rows positions x row_len values (kv_lora_rank 512
+    + rope dim 64) quantised to 34-byte blocks and dequantised back; rates
+    in algorithmic bytes (f32 in / out, 34 B per 32 values) per kernel."""
+    x = rng.standard_normal((n_rows, row_len)).astype(np.float32)
+    nbytes = n_rows * ((row_len + 31) // 32) * 34
+    dx = mm.DeviceArray.from_numpy(ctx, x)
+    db = mm.DeviceArray(ctx, nbytes)
+    dy = mm.DeviceArray(ctx, x.nbytes)
+    st = ctx.stream
+    q = lambda: ctx.quantize_q8_0_rows_dev(db, dx, row_len, n_rows, row_len)
+    d = lambda: ctx.dequantize_q8_0_rows_dev(dy, row_len, db, n_rows, row_len)
+    for _ in range(3):
+        q()
+        d()
+    ctx.synchronize()
+    out = {}
+    for name, fn in (("quantize", q), ("dequantize", d)):
+        us = float(np.median([ev.time_ms(st, lambda: [fn() for _ in range(reps)]) / reps for _ in range(5)])) * 1e3
+        gbs = (x.nbytes + nbytes) / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    for a in (dx, db, dy):
+        a.free()
+    out["workload"] = (f"{n_rows} positions x {row_len} f32 (kv_lora 512 + rope 64) <-> Q8_0 blocks; "
+                       f"{x.nbytes + nbytes} algorithmic bytes per kernel call")
+    return out
+
+
+def cpu_kv_codec_baseline(rng, seconds=2.0, row_len=576):
+    """Oracle quantizeQ8_0 per row on one core (KVCache.put's loop), bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    x = rng.standard_normal((4096, row_len)).astype(np.float32)
+    nbytes = x.nbytes + 4096 * ((row_len + 31) // 32) * 34
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        orc.quantize_q8_0_rows(x, row_len)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(nbytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n} x quantise 4096 positions x {row_len} values in {dt:.1f} s"}
+
+
 def cpu_gemv_baseline(seconds):
     """Oracle IQ2_XXS GEMV (dequantize + f32 GEMV, one thread), bounded sample:
     alternating [1536 x 2048] and [2048 x 1536] matrices for about `seconds`."""
@@ -369,8 +414,10 @@ def main():
                       "workload": "hidden 2048, 64 IQ2_XXS experts (1536) top-4 + shared, f32 router; "
                                   "batch 64 with Zipf(1.1) routing; cold: eight layers rotate (batch 1 also over "
                                   "61 tokens); warm: one layer, one input"}
+    out["kv_q8_codec"] = kv_codec_section(ctx, ev, rng)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_gemv_baseline(args.cpu_seconds)
+        out["kv_q8_codec"]["cpu_quantize"] = cpu_kv_codec_baseline(rng)
         if weights is not None:
             out["cpu_moe"] = cpu_moe_baseline(weights, args.cpu_moe_tokens)
     ctx.close()

@@ -136,6 +136,15 @@ int mmhip_batch_mat_mul(mmhip_ctx* ctx, float* out_host, const void* ptr_host,
                         uint64_t batch, uint64_t in_dim);
 int mmhip_dequantize(mmhip_ctx* ctx, float* out_host, const void* data_host,
                      uint32_t type, uint64_t n_elements);
+/* quantizeQ8_0 (dequant.zig:98-130): n floats -> ceil(n / 32) raw Q8_0
+ * blocks of 34 bytes (per block: d = max|x| / 127 stored as f16, q = x / d
+ * rounded half away from zero, clamped to +-127; the last block padded with
+ * zeros). Bit-exact with the CPU path; where a block scale falls in the f16
+ * subnormal range (max|x| < 127 * 2^-14), for which the reference's f32ToF16
+ * has no defined result (its shift overflows the 10-bit field), the scale is
+ * the subnormal value truncated toward zero. A NaN value quantises to 0. */
+int mmhip_quantize_q8_0(mmhip_ctx* ctx, void* blocks_host, const float* x_host,
+                        uint64_t n_elements);
 /* Drop the resident copy keyed by ptr_host (all types/shapes). */
 int mmhip_forget(mmhip_ctx* ctx, const void* ptr_host);
 
@@ -146,6 +155,17 @@ int mmhip_forget(mmhip_ctx* ctx, const void* ptr_host);
 /* dequantize from raw GGUF bytes in device memory; bit-exact. */
 int mmhip_dequantize_dev(mmhip_ctx* ctx, float* out_dev, const void* raw_dev,
                          uint32_t type, uint64_t n_elements);
+/* KVCache.put's Q8_0 branch (kv_cache.zig:289-349) for n_rows positions at
+ * once: row r of row_len floats (x_dev + r * x_stride) -> ceil(row_len / 32)
+ * blocks at blocks_dev + r * ceil(row_len / 32) * 34, as mmhip_quantize_q8_0
+ * per row. blocks_dev must be 4-byte aligned. */
+int mmhip_quantize_q8_0_rows_dev(mmhip_ctx* ctx, void* blocks_dev, const float* x_dev,
+                                 uint64_t x_stride, uint64_t n_rows, uint32_t row_len);
+/* getKVCompressed / getKPe's Q8_0 branch (kv_cache.zig:225-273) for n_rows
+ * positions: out_dev[r * out_stride + c] = f16ToF32(d) * q; bit-exact.
+ * blocks_dev must be 2-byte aligned. */
+int mmhip_dequantize_q8_0_rows_dev(mmhip_ctx* ctx, float* out_dev, uint64_t out_stride,
+                                   const void* blocks_dev, uint64_t n_rows, uint32_t row_len);
 /* y[rows] = W[mat] . x[cols] for one matrix of a weight. */
 int mmhip_gemv_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat,
                    const float* x_dev, float* y_dev);

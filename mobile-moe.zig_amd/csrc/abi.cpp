@@ -314,6 +314,62 @@ int mmhip_dequantize_dev(mmhip_ctx* ctx, float* out_dev, const void* raw_dev, ui
     return e == hipSuccess ? MMHIP_OK : hip_fail(e, "dequantize_dev");
 }
 
+int mmhip_quantize_q8_0_rows_dev(mmhip_ctx* ctx, void* blocks_dev, const float* x_dev, uint64_t x_stride,
+                                 uint64_t n_rows, uint32_t row_len) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (n_rows == 0 || row_len == 0) return MMHIP_OK;
+    if (!blocks_dev || !x_dev || x_stride < row_len) {
+        set_error(MMHIP_ERR_INVALID, "quantize_q8_0_rows_dev: null pointer or x_stride < row_len");
+        return MMHIP_ERR_INVALID;
+    }
+    if (reinterpret_cast<uintptr_t>(blocks_dev) & 3u) {
+        set_error(MMHIP_ERR_INVALID, "quantize_q8_0_rows_dev: blocks_dev must be 4-byte aligned");
+        return MMHIP_ERR_INVALID;
+    }
+    hipError_t e = launch_quantize_q8_0_rows(x_dev, x_stride, n_rows, row_len, blocks_dev, ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "quantize_q8_0_rows_dev");
+}
+
+int mmhip_dequantize_q8_0_rows_dev(mmhip_ctx* ctx, float* out_dev, uint64_t out_stride, const void* blocks_dev,
+                                   uint64_t n_rows, uint32_t row_len) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (n_rows == 0 || row_len == 0) return MMHIP_OK;
+    if (!blocks_dev || !out_dev || out_stride < row_len) {
+        set_error(MMHIP_ERR_INVALID, "dequantize_q8_0_rows_dev: null pointer or out_stride < row_len");
+        return MMHIP_ERR_INVALID;
+    }
+    if (reinterpret_cast<uintptr_t>(blocks_dev) & 1u) {
+        set_error(MMHIP_ERR_INVALID, "dequantize_q8_0_rows_dev: blocks_dev must be 2-byte aligned");
+        return MMHIP_ERR_INVALID;
+    }
+    hipError_t e = launch_dequantize_q8_0_rows(blocks_dev, n_rows, row_len, out_dev, out_stride, ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "dequantize_q8_0_rows_dev");
+}
+
+int mmhip_quantize_q8_0(mmhip_ctx* ctx, void* blocks_host, const float* x_host, uint64_t n) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (n == 0) return MMHIP_OK;
+    if (!blocks_host || !x_host) {
+        set_error(MMHIP_ERR_INVALID, "quantize_q8_0: null pointer");
+        return MMHIP_ERR_INVALID;
+    }
+    const uint64_t out_bytes = (n + 31) / 32 * 34;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipError_t e = ctx->d_out.ensure(n * 4);
+    if (e == hipSuccess) e = ctx->d_raw.ensure(out_bytes);
+    if (e != hipSuccess) return hip_fail(e, "quantize_q8_0: scratch");
+    e = hipMemcpyAsync(ctx->d_out.p, x_host, n * 4, hipMemcpyHostToDevice, ctx->stream);
+    // One row of n values: the blocks of quantizeQ8_0 over the whole array.
+    if (e == hipSuccess) {
+        if (n > 0xFFFFFFFFull) e = hipErrorInvalidValue;
+        else e = launch_quantize_q8_0_rows(static_cast<const float*>(ctx->d_out.p), n, 1, (uint32_t)n, ctx->d_raw.p,
+                                           ctx->stream);
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(blocks_host, ctx->d_raw.p, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "quantize_q8_0");
+}
+
 int mmhip_gemv_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x_dev, float* y_dev) {
     return mmhip_gemv_batched_dev(ctx, w, mat, 1, x_dev, 0, y_dev, 0);
 }

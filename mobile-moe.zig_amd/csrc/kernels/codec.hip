@@ -196,6 +196,193 @@ __global__ __launch_bounds__(256) void quantize_wide_kernel(const float* __restr
                              s_stride);
 }
 
+// ---- Q8_0 codec over rows (quantizeQ8_0, dequant.zig:98-130; the Q8_0
+// branches of KVCache.put / getKVCompressed / getKPe, kv_cache.zig:225-349) ----
+//
+// Row r of row_len values maps to ceil(row_len / 32) blocks of 34 bytes at
+// r * ceil(row_len / 32) * 34; a row's last block is padded with zeros. One
+// wave covers 8 consecutive blocks of the flattened (row, block) order: lane
+// (k, j) holds values 4j..4j+3 of block k, so the wave reads 1 KiB of
+// activations (contiguous within a row) and writes 272 bytes, assembled in
+// LDS and stored as dwords (a wave's output starts at a multiple of 272).
+
+// f32ToF16 (dequant.zig:50-95) as the quantiser stores a block scale: round
+// to nearest even on the normal range, 0 for f32 subnormals and below 2^-25,
+// Inf / NaN kept. On the f16 subnormal range the reference shifts the
+// significand by 1 - e16, which overflows the 10-bit field (a trap in safe
+// builds, so it defines no result); this takes the branch's evident intent,
+// a shift by 14 - e16: the subnormal value truncated toward zero.
+__device__ __forceinline__ uint32_t f32_to_f16_scale(float v) {
+    const uint32_t bits = __float_as_uint(v);
+    const uint32_t er = (bits >> 23) & 0xFFu, mant = bits & 0x7FFFFFu;
+    uint32_t e = 0, m = 0;
+    if (er == 0xFFu) {
+        e = 0x1Fu;
+        m = mant >> 13;
+        if (mant != 0 && m == 0) m = 1;
+    } else if (er != 0) {
+        const int e16 = (int)er - 112;
+        if (e16 >= 31) {
+            e = 0x1Fu;
+        } else if (e16 <= 0) {
+            if (e16 >= -10) m = (mant | 0x800000u) >> (uint32_t)(14 - e16);
+        } else {
+            e = (uint32_t)e16;
+            m = mant >> 13;
+            const uint32_t rb = mant & 0x1FFFu;
+            if (rb > 0x1000u || (rb == 0x1000u && (m & 1u))) {
+                ++m;
+                if (m == 0x400u) {
+                    m = 0;
+                    ++e;
+                }
+            }
+        }
+    }
+    return ((bits >> 31) << 15) | (e << 10) | m;
+}
+
+// Tiles of 256 consecutive blocks (8,704 bytes: 68 whole 128-byte lines of
+// the block array) per 512-thread workgroup: lane (k, j) holds values
+// 4j..4j+3 of blocks k + 64u, u < 4, all four loads issued before any use
+// (~128 KiB in flight per CU at four workgroups, which HBM latency needs);
+// workgroups loop over tiles.
+constexpr int kQ8Threads = 512;
+constexpr uint32_t kQ8Groups = kQ8Threads / 8;  // blocks per pass of the workgroup
+constexpr uint32_t kQ8Per = 4;                  // passes per tile
+constexpr uint32_t kQ8TileBlocks = kQ8Groups * kQ8Per;
+constexpr uint32_t kQ8TileWords = kQ8TileBlocks * 34 / 4;
+constexpr uint64_t kQ8Grid = 256 * 4;  // workgroups: 4 per CU of MI355X
+
+// Row and block-in-row of block b0 + k, from (row0, blk0) = b0 split once per
+// tile: (blk0 + k) / bpr by a float reciprocal, corrected by one step (the
+// quotient is below 2^16, so the estimate is off by at most one).
+struct RowBlock {
+    uint64_t row;
+    uint32_t blk;
+};
+__device__ __forceinline__ RowBlock row_block(uint64_t row0, uint32_t blk0, uint32_t k, uint32_t bpr, float inv_bpr) {
+    const uint32_t t = blk0 + k;
+    uint32_t q = (uint32_t)((float)t * inv_bpr);
+    if (q * bpr > t) --q;
+    if ((q + 1) * bpr <= t) ++q;
+    return RowBlock{row0 + q, t - q * bpr};
+}
+
+__global__ __launch_bounds__(kQ8Threads) void quantize_q8_0_rows_kernel(const float* __restrict__ x,
+                                                                        uint64_t x_stride, uint64_t n_rows,
+                                                                        uint32_t row_len, bool vec,
+                                                                        uint8_t* __restrict__ out) {
+    __shared__ __align__(16) uint32_t stage[kQ8TileWords];
+    uint8_t* const st = reinterpret_cast<uint8_t*>(stage);
+    const uint32_t k = threadIdx.x >> 3, j = threadIdx.x & 7;
+    const uint32_t bpr = (row_len + 31) / 32;
+    const float inv_bpr = 1.0f / (float)bpr;
+    const uint64_t nblk = n_rows * bpr;
+    const uint64_t n_tiles = (nblk + kQ8TileBlocks - 1) / kQ8TileBlocks;
+    for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const uint64_t b0 = tile * kQ8TileBlocks;
+        const uint64_t row0 = b0 / bpr;
+        const uint32_t blk0 = (uint32_t)(b0 % bpr);
+        float v[kQ8Per][4];
+        uint32_t n_live[kQ8Per];
+#pragma unroll
+        for (uint32_t u = 0; u < kQ8Per; ++u) {
+            const uint32_t kk = k + kQ8Groups * u;
+            const RowBlock rb = row_block(row0, blk0, kk, bpr, inv_bpr);
+            const uint32_t c0 = rb.blk * 32 + 4 * j;
+            // Values past the row (or past the last block) count as absent.
+            n_live[u] = b0 + kk < nblk ? (c0 < row_len ? min(row_len - c0, 4u) : 0u) : 0u;
+            const float* src = x + rb.row * x_stride + c0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[u][e] = 0.0f;
+            if (vec && n_live[u] == 4) {
+                const float4 q = *reinterpret_cast<const float4*>(src);
+                v[u][0] = q.x;
+                v[u][1] = q.y;
+                v[u][2] = q.z;
+                v[u][3] = q.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if ((uint32_t)e < n_live[u]) v[u][e] = src[e];
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kQ8Per; ++u) {
+            // The block's largest |x| (a NaN never compares greater).
+            float m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float av = fabsf(v[u][e]);
+                m = ((uint32_t)e < n_live[u] && av > m) ? av : m;
+            }
+            m = max8_lanes(m);
+            const float d = m > 0.0f ? m / 127.0f : 0.0f;
+            uint32_t q4 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // The f32 d, half away from zero (@round). The exact quotient
+                // is needed (a rounded estimate can land on the other side of
+                // a half-integer); guarding an estimate measured slower.
+                const float quo = v[u][e] / d;
+                float r = roundf(quo);
+                r = (r == r && d > 0.0f && (uint32_t)e < n_live[u]) ? r : 0.0f;  // NaN input (@intFromFloat traps)
+                const int q = (int)fminf(fmaxf(r, -127.0f), 127.0f);
+                q4 |= (uint32_t)(q & 0xFF) << (8 * e);
+            }
+            const uint32_t kk = k + kQ8Groups * u;
+            if (b0 + kk < nblk) {
+                *reinterpret_cast<uint16_t*>(st + kk * 34 + 2 + 4 * j) = (uint16_t)(q4 & 0xFFFFu);
+                *reinterpret_cast<uint16_t*>(st + kk * 34 + 4 + 4 * j) = (uint16_t)(q4 >> 16);
+                if (j == 0) *reinterpret_cast<uint16_t*>(st + kk * 34) = (uint16_t)f32_to_f16_scale(d);
+            }
+        }
+        lds_barrier();
+        const uint32_t bytes = (uint32_t)min<uint64_t>(kQ8TileBlocks, nblk - b0) * 34;
+        uint8_t* dst = out + b0 * 34;  // 4-byte aligned: b0 * 34 is a multiple of 8,704
+        for (uint32_t i = threadIdx.x; i < bytes / 4; i += kQ8Threads)
+            reinterpret_cast<uint32_t*>(dst)[i] = stage[i];
+        if ((bytes & 3u) && threadIdx.x == 0)
+            *reinterpret_cast<uint16_t*>(dst + bytes - 2) = *reinterpret_cast<const uint16_t*>(st + bytes - 2);
+        lds_barrier();  // the tile's LDS is free again
+    }
+}
+
+// Rows of row_len values back from their blocks: out[r * out_stride + c] =
+// f16ToF32(d) * q (dequantizeQ8_0, dequant.zig:379-390; exact in f32). One
+// short-lived wave per 8 blocks (lane (k, j): values 4j..4j+3 of block k):
+// the output is 4x the input, and many small workgroups keep the stores
+// streaming better than a loop over tiles (4.35 vs 3.5 TB/s measured).
+constexpr int kQ8DqThreads = 256;
+__global__ __launch_bounds__(kQ8DqThreads) void dequantize_q8_0_rows_kernel(const uint8_t* __restrict__ blocks,
+                                                                            uint64_t n_rows, uint32_t row_len,
+                                                                            bool vec, float* __restrict__ out,
+                                                                            uint64_t out_stride) {
+    const uint32_t k = (threadIdx.x >> 3) & 7, j = threadIdx.x & 7;
+    const uint32_t bpr = (row_len + 31) / 32;
+    const uint64_t nblk = n_rows * bpr;
+    const uint64_t b0 = ((uint64_t)blockIdx.x * (kQ8DqThreads / 64) + (threadIdx.x >> 6)) * 8;
+    if (b0 + k >= nblk) return;
+    const RowBlock rb = row_block(b0 / bpr, (uint32_t)(b0 % bpr), k, bpr, 1.0f / (float)bpr);
+    const uint8_t* blk = blocks + (b0 + k) * 34;
+    const float d = f16_scale(*reinterpret_cast<const uint16_t*>(blk));
+    const uint32_t q4 = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + 2 + 4 * j) |
+                        ((uint32_t)*reinterpret_cast<const uint16_t*>(blk + 4 + 4 * j) << 16);
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = d * (float)(int8_t)(q4 >> (8 * e));
+    const uint32_t c0 = rb.blk * 32 + 4 * j;
+    float* dst = out + rb.row * out_stride + c0;
+    if (vec && c0 + 4 <= row_len) {
+        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (c0 + e < row_len) dst[e] = v[e];
+    }
+}
+
 }  // namespace
 
 hipError_t launch_dequant(const void* raw, uint32_t type, uint64_t n, float* out, hipStream_t s) {
@@ -268,6 +455,34 @@ hipError_t launch_quantize_silu(const float* src, uint64_t src_stride, uint64_t 
     }
     quantize_silu_kernel<<<(unsigned)((threads + bs - 1) / bs), bs, 0, s>>>(
         src, src_stride, u_off, n_rows, n_rows_max, cols, cols_pad, q.hi, q.lo, q.scale, q.stride, q.scale_stride);
+    return hipGetLastError();
+}
+
+}  // namespace mmhip
+
+namespace mmhip {
+
+hipError_t launch_quantize_q8_0_rows(const float* x, uint64_t x_stride, uint64_t n_rows, uint32_t row_len, void* out,
+                                     hipStream_t s) {
+    if (n_rows == 0 || row_len == 0) return hipSuccess;
+    if (reinterpret_cast<uintptr_t>(out) & 3u) return hipErrorInvalidValue;
+    const uint64_t tiles = (n_rows * ((row_len + 31) / 32) + kQ8TileBlocks - 1) / kQ8TileBlocks;
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && x_stride % 4 == 0;
+    const unsigned grid = (unsigned)(tiles < kQ8Grid ? tiles : kQ8Grid);
+    quantize_q8_0_rows_kernel<<<grid, kQ8Threads, 0, s>>>(x, x_stride, n_rows, row_len, vec,
+                                                           static_cast<uint8_t*>(out));
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize_q8_0_rows(const void* blocks, uint64_t n_rows, uint32_t row_len, float* out,
+                                       uint64_t out_stride, hipStream_t s) {
+    if (n_rows == 0 || row_len == 0) return hipSuccess;
+    if (reinterpret_cast<uintptr_t>(blocks) & 1u) return hipErrorInvalidValue;
+    const uint64_t nblk = n_rows * ((row_len + 31) / 32);
+    const uint64_t per_wg = (uint64_t)(kQ8DqThreads / 64) * 8;
+    const bool vec = (reinterpret_cast<uintptr_t>(out) & 15u) == 0 && out_stride % 4 == 0;
+    dequantize_q8_0_rows_kernel<<<(unsigned)((nblk + per_wg - 1) / per_wg), kQ8DqThreads, 0, s>>>(
+        static_cast<const uint8_t*>(blocks), n_rows, row_len, vec, out, out_stride);
     return hipGetLastError();
 }
 

@@ -102,6 +102,15 @@ struct GemvArgs {
 // Raw GGUF bytes -> f32, bit-exact (dequant.zig:316-390, 632-659).
 hipError_t launch_dequant(const void* raw, uint32_t ggml_type, uint64_t n, float* out, hipStream_t s);
 
+// Q8_0 codec over rows (quantizeQ8_0, dequant.zig:98-130; KVCache.put /
+// getKVCompressed's Q8_0 branches): row r of row_len floats <-> ceil(row_len
+// / 32) 34-byte blocks at r * ceil(row_len / 32) * 34. out of the quantiser
+// 4-byte aligned, blocks of the dequantiser 2-byte aligned.
+hipError_t launch_quantize_q8_0_rows(const float* x, uint64_t x_stride, uint64_t n_rows, uint32_t row_len, void* out,
+                                     hipStream_t s);
+hipError_t launch_dequantize_q8_0_rows(const void* blocks, uint64_t n_rows, uint32_t row_len, float* out,
+                                       uint64_t out_stride, hipStream_t s);
+
 // Raw GGUF bytes -> tile layout.
 hipError_t launch_repack(const void* raw, const TileGeom& g, uint4* recs, uint16_t* dvals, hipStream_t s);
 

@@ -96,6 +96,9 @@ _SIGS = {
     "mmhip_dequantize": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u32, _u64]),
     "mmhip_forget": (ctypes.c_int, [_c_void_p, _c_void_p]),
     "mmhip_dequantize_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u32, _u64]),
+    "mmhip_quantize_q8_0": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u64]),
+    "mmhip_quantize_q8_0_rows_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u64, _u64, _u32]),
+    "mmhip_dequantize_q8_0_rows_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _u64, _u32]),
     "mmhip_gemv_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _c_void_p]),
     "mmhip_gemv_batched_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _u64, _c_void_p, _u64,
                                               _c_void_p, _u64]),
@@ -289,6 +292,13 @@ class Context:
         check(self.lib.mmhip_dequantize(self.handle, _ptr(out), _ptr(raw), ggml_type, n), "mmhip_dequantize")
         return out
 
+    def quantize_q8_0(self, x: np.ndarray) -> np.ndarray:
+        """quantizeQ8_0 (dequant.zig:98-130) on the device: raw 34-byte blocks."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        out = np.empty(((x.size + 31) // 32) * 34, dtype=np.uint8)
+        check(self.lib.mmhip_quantize_q8_0(self.handle, _ptr(out), _ptr(x), x.size), "mmhip_quantize_q8_0")
+        return out
+
     def forget(self, raw: np.ndarray):
         check(self.lib.mmhip_forget(self.handle, _ptr(raw)), "mmhip_forget")
 
@@ -303,6 +313,19 @@ class Context:
 
     def dequantize_dev(self, out: DeviceArray, raw: DeviceArray, ggml_type: int, n: int):
         check(self.lib.mmhip_dequantize_dev(self.handle, out.ptr, raw.ptr, ggml_type, n), "mmhip_dequantize_dev")
+
+    def quantize_q8_0_rows_dev(self, blocks: DeviceArray, x: DeviceArray, x_stride: int, n_rows: int, row_len: int,
+                               blocks_offset: int = 0, x_offset: int = 0):
+        """KVCache.put's Q8_0 branch for n_rows rows (byte offsets into the buffers)."""
+        check(self.lib.mmhip_quantize_q8_0_rows_dev(self.handle, blocks.ptr + blocks_offset, x.ptr + x_offset,
+                                                    x_stride, n_rows, row_len), "mmhip_quantize_q8_0_rows_dev")
+
+    def dequantize_q8_0_rows_dev(self, out: DeviceArray, out_stride: int, blocks: DeviceArray, n_rows: int,
+                                 row_len: int, out_offset: int = 0, blocks_offset: int = 0):
+        """getKVCompressed / getKPe's Q8_0 branch for n_rows rows."""
+        check(self.lib.mmhip_dequantize_q8_0_rows_dev(self.handle, out.ptr + out_offset, out_stride,
+                                                      blocks.ptr + blocks_offset, n_rows, row_len),
+              "mmhip_dequantize_q8_0_rows_dev")
 
 
 class MoeLayer:

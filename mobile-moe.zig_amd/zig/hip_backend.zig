@@ -13,6 +13,7 @@
 
 const std = @import("std");
 const gguf = @import("gguf.zig");
+const dequant = @import("dequant.zig");
 
 // ---- C ABI (include/mmhip.h) ----
 
@@ -100,6 +101,9 @@ extern fn mmhip_mat_vec_mul(ctx: *Ctx, out_host: [*]f32, ptr_host: ?*const anyop
 extern fn mmhip_batch_mat_mul(ctx: *Ctx, out_host: [*]f32, ptr_host: ?*const anyopaque, type_: u32, in_host: [*]const f32, out_dim: u64, batch: u64, in_dim: u64) c_int;
 extern fn mmhip_dequantize(ctx: *Ctx, out_host: [*]f32, data_host: ?*const anyopaque, type_: u32, n_elements: u64) c_int;
 extern fn mmhip_forget(ctx: *Ctx, ptr_host: ?*const anyopaque) c_int;
+extern fn mmhip_quantize_q8_0(ctx: *Ctx, blocks_host: ?*anyopaque, x_host: [*]const f32, n_elements: u64) c_int;
+extern fn mmhip_quantize_q8_0_rows_dev(ctx: *Ctx, blocks_dev: ?*anyopaque, x_dev: ?*const anyopaque, x_stride: u64, n_rows: u64, row_len: u32) c_int;
+extern fn mmhip_dequantize_q8_0_rows_dev(ctx: *Ctx, out_dev: ?*anyopaque, out_stride: u64, blocks_dev: ?*const anyopaque, n_rows: u64, row_len: u32) c_int;
 extern fn mmhip_dequantize_dev(ctx: *Ctx, out_dev: ?*anyopaque, raw_dev: ?*const anyopaque, type_: u32, n_elements: u64) c_int;
 extern fn mmhip_gemv_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque) c_int;
 extern fn mmhip_gemv_batched_dev(ctx: *Ctx, w: *const Weight, first: u64, n_mats: u64, x_dev: ?*const anyopaque, x_stride: u64, y_dev: ?*anyopaque, y_stride: u64) c_int;
@@ -188,6 +192,26 @@ pub const HipBackend = struct {
     /// dequant.dequantize (dequant.zig:632-659) on the device, bit-exact.
     pub fn dequantize(self: *Self, out: []f32, data: [*]const u8, type_: gguf.GgmlType) !void {
         try check(mmhip_dequantize(self.ctx, out.ptr, data, @intFromEnum(type_), out.len));
+    }
+
+    /// dequant.quantizeQ8_0 (dequant.zig:98-130) on the device: `blocks`
+    /// receives (data.len + 31) / 32 blocks (caller-owned, unlike the
+    /// reference's allocating version).
+    pub fn quantizeQ8_0(self: *Self, blocks: []dequant.BlockQ8_0, data: []const f32) !void {
+        std.debug.assert(blocks.len == (data.len + 31) / 32);
+        try check(mmhip_quantize_q8_0(self.ctx, blocks.ptr, data.ptr, data.len));
+    }
+
+    /// KVCache.put's Q8_0 branch (kv_cache.zig:289-349) for n_rows device
+    /// rows at once (e.g. a prefill's kv_comp rows of kv_lora_rank values).
+    pub fn quantizeRowsQ8_0Dev(self: *Self, blocks_dev: *anyopaque, x_dev: *const anyopaque, x_stride: u64, n_rows: u64, row_len: u32) !void {
+        try check(mmhip_quantize_q8_0_rows_dev(self.ctx, blocks_dev, x_dev, x_stride, n_rows, row_len));
+    }
+
+    /// getKVCompressed / getKPe's Q8_0 branch (kv_cache.zig:225-273) for
+    /// n_rows device rows at once.
+    pub fn dequantizeRowsQ8_0Dev(self: *Self, out_dev: *anyopaque, out_stride: u64, blocks_dev: *const anyopaque, n_rows: u64, row_len: u32) !void {
+        try check(mmhip_dequantize_q8_0_rows_dev(self.ctx, out_dev, out_stride, blocks_dev, n_rows, row_len));
     }
 
     /// Drops the resident copy of a weight (e.g. before unmapping the file).

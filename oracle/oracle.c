@@ -94,6 +94,67 @@ uint16_t orc_f32_to_f16(float v, int* defect) {
     return (uint16_t)((sign << 15) | (e << 10) | m);
 }
 
+/* f32ToF16 as quantizeQ8_0 / KVCache.put store a block scale. Same as
+ * orc_f32_to_f16 except where the reference's subnormal branch overflows
+ * (above; a trap in safe builds, so the reference defines no result there):
+ * this uses the branch's evident intent, the significand shifted by
+ * 14 - e16, i.e. the subnormal result truncated toward zero. */
+static uint16_t f32_to_f16_scale(float v) {
+    int defect = 0;
+    uint16_t h = orc_f32_to_f16(v, &defect);
+    if (!defect) return h;
+    uint32_t bits = f32_to_bits(v);
+    int e16 = (int)((bits >> 23) & 0xFFu) - 127 + 15;
+    uint32_t m = ((bits & 0x7FFFFFu) | 0x800000u) >> (uint32_t)(14 - e16);
+    return (uint16_t)((((bits >> 31) & 1u) << 15) | m);
+}
+
+/* quantizeQ8_0, dequant.zig:98-130, which is also KVCache.put's Q8_0 branch
+ * (kv_cache.zig:289-349): per 32-value block, max_abs = the largest |x| of
+ * the block's values (a NaN never compares greater), d = max_abs / 127 in
+ * f32 (0 when max_abs is 0), stored as f16 (f32_to_f16_scale); q = x / d in
+ * f32 rounded half away from zero (@round) and clamped to [-127, 127], with
+ * the f32 d, not the stored f16 one; q = 0 where d is 0 and past n. A NaN
+ * value gets q = 0 (the reference's @intFromFloat traps there). */
+void orc_quantize_q8_0(const float* x, uint64_t n, uint8_t* out) {
+    uint64_t nb = (n + 31) / 32;
+    for (uint64_t b = 0; b < nb; ++b) {
+        uint8_t* blk = out + b * 34;
+        float max_abs = 0.0f;
+        for (uint64_t j = 0; j < 32 && b * 32 + j < n; ++j) {
+            float av = fabsf(x[b * 32 + j]);
+            if (av > max_abs) max_abs = av;
+        }
+        float d = max_abs > 0.0f ? max_abs / 127.0f : 0.0f;
+        uint16_t h = f32_to_f16_scale(d);
+        blk[0] = (uint8_t)(h & 0xFFu);
+        blk[1] = (uint8_t)(h >> 8);
+        for (uint64_t j = 0; j < 32; ++j) {
+            int q = 0;
+            if (b * 32 + j < n && d > 0.0f) {
+                float r = roundf(x[b * 32 + j] / d);
+                if (r != r) r = 0.0f;
+                if (r > 127.0f) r = 127.0f;
+                if (r < -127.0f) r = -127.0f;
+                q = (int)r;
+            }
+            blk[2 + j] = (uint8_t)(int8_t)q;
+        }
+    }
+}
+
+/* KVCache.put / getKVCompressed per position (kv_cache.zig:232-246, 289-349):
+ * row r of row_len values (x + r * x_stride) <-> ceil(row_len / 32) blocks at
+ * out + r * ceil(row_len / 32) * 34. */
+void orc_quantize_q8_0_rows(const float* x, uint64_t x_stride, uint64_t n_rows, uint32_t row_len, uint8_t* out) {
+    uint64_t rb = ((uint64_t)row_len + 31) / 32 * 34;
+    for (uint64_t r = 0; r < n_rows; ++r) orc_quantize_q8_0(x + r * x_stride, row_len, out + r * rb);
+}
+void orc_dequantize_q8_0_rows(const uint8_t* blocks, uint64_t n_rows, uint32_t row_len, float* out) {
+    uint64_t rb = ((uint64_t)row_len + 31) / 32 * 34;
+    for (uint64_t r = 0; r < n_rows; ++r) orc_dequantize_q8_0(blocks + r * rb, row_len, out + r * row_len);
+}
+
 /* GgmlType.blockSize / blockBytes / tensorBytes, gguf.zig:59-117 (the types
  * on this path). */
 uint64_t orc_block_size(uint32_t type) {

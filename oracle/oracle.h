@@ -21,6 +21,13 @@
  *                           reference defect (see the function) and is only
  *                           checked to report it.
  *   orc_dequantize_q8_0     closed form d*q (exact in f32) on all 65,536 d codes.
+ *   orc_quantize_q8_0       reference KAT kv_cache.zig:686-719 (put/get round
+ *                           trip within 5% + 1e-2), stored d = f32ToF16(max/127)
+ *                           (normal range: the pinned converter; subnormal:
+ *                           exact integer truncation), q = the nearest integer
+ *                           to x/d with ties away from zero (searched over
+ *                           [-127, 127]), +-127 at each block's largest |x|,
+ *                           zero blocks and padding.
  *   orc_dequantize_iq2xxs   hand-derived special cases (all-zero block = 1.0,
  *                           byte order of grid entries, sign bit positions,
  *                           ls=15 scale), codebook invariants, ksigns closed form.
@@ -64,6 +71,9 @@ uint64_t orc_tensor_bytes(uint32_t type, uint64_t n_elements);
 uint64_t orc_iq2xxs_grid(uint32_t idx);
 uint8_t orc_ksigns(uint32_t code);
 void orc_dequantize_q8_0(const uint8_t* data, uint64_t n_elements, float* out);
+void orc_quantize_q8_0(const float* x, uint64_t n_elements, uint8_t* out);
+void orc_quantize_q8_0_rows(const float* x, uint64_t x_stride, uint64_t n_rows, uint32_t row_len, uint8_t* out);
+void orc_dequantize_q8_0_rows(const uint8_t* blocks, uint64_t n_rows, uint32_t row_len, float* out);
 void orc_dequantize_iq2xxs_block(const uint8_t* block, float* out256);
 void orc_dequantize_iq2xxs(const uint8_t* data, uint64_t n_elements, float* out);
 int orc_dequantize(const uint8_t* data, uint32_t type, uint64_t n_elements, float* out);

@@ -46,6 +46,9 @@ _SIGS = {
     "orc_iq2xxs_grid": (_u64, [_u32]),
     "orc_ksigns": (ctypes.c_uint8, [_u32]),
     "orc_dequantize_q8_0": (None, [_vp, _u64, _vp]),
+    "orc_quantize_q8_0": (None, [_vp, _u64, _vp]),
+    "orc_quantize_q8_0_rows": (None, [_vp, _u64, _u64, _u32, _vp]),
+    "orc_dequantize_q8_0_rows": (None, [_vp, _u64, _u32, _vp]),
     "orc_dequantize_iq2xxs_block": (None, [_vp, _vp]),
     "orc_dequantize_iq2xxs": (None, [_vp, _u64, _vp]),
     "orc_dequantize": (ctypes.c_int, [_vp, _u32, _u64, _vp]),
@@ -96,6 +99,31 @@ def f32_to_f16(v: float):
     d = ctypes.c_int(0)
     r = lib().orc_f32_to_f16(v, ctypes.byref(d))
     return r, bool(d.value)
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    """quantizeQ8_0 (dequant.zig:98-130): f32 values -> raw 34-byte blocks."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(((x.size + 31) // 32) * 34, dtype=np.uint8)
+    lib().orc_quantize_q8_0(_p(x), x.size, _p(out))
+    return out
+
+
+def quantize_q8_0_rows(x: np.ndarray, row_len: int) -> np.ndarray:
+    """KVCache.put's Q8_0 branch per row: [n_rows][row_len] f32 -> blocks."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n_rows = x.size // row_len
+    out = np.empty(n_rows * ((row_len + 31) // 32) * 34, dtype=np.uint8)
+    lib().orc_quantize_q8_0_rows(_p(x), row_len, n_rows, row_len, _p(out))
+    return out
+
+
+def dequantize_q8_0_rows(blocks: np.ndarray, n_rows: int, row_len: int) -> np.ndarray:
+    """getKVCompressed / getKPe's dequantization per row."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty((n_rows, row_len), dtype=np.float32)
+    lib().orc_dequantize_q8_0_rows(_p(blocks), n_rows, row_len, _p(out))
+    return out
 
 
 def ksigns(code: int) -> int:
