@@ -257,6 +257,47 @@ def cpu_kv_codec_baseline(rng, seconds=2.0, row_len=576):
             "sample": f"{n} x quantise 4096 positions x {row_len} values in {dt:.1f} s"}
 
 
+def logits_section(ctx, ev, rng, reps=20, vocab=154880, hidden=HIDDEN):
+    """computeLogits + sampleGreedy (inference.zig:1189-1197, 376-386): the
+    output projection GEMV [vocab x hidden] in Q8_0 and IQ2_XXS (the GGUF's
+    type decides), weights rotating over at least 300 MB, then the greedy
+    argmax over the logits on the device."""
+    x = mm.DeviceArray.from_numpy(ctx, rng.standard_normal(hidden).astype(np.float32))
+    y = mm.DeviceArray(ctx, vocab * 4)
+    tok = mm.DeviceArray(ctx, 4)
+    st = ctx.stream
+    out = {"workload": f"output projection [{vocab} x {hidden}] GEMV + greedy argmax over {vocab} logits"}
+    for name, t in (("q8_0", mm.Q8_0), ("iq2_xxs", mm.IQ2_XXS)):
+        raw = mm.make_weight(rng, t, vocab, hidden)
+        n_sets = max(1, int(np.ceil(300e6 / raw.nbytes)))
+        ws = [ctx.upload(raw, t, vocab, hidden) for _ in range(n_sets)]
+        k = [0]
+
+        def one():
+            ctx.gemv_batched_dev(ws[k[0] % n_sets], 0, 1, x, 0, y, 0)
+            k[0] += 1
+
+        for _ in range(2 * n_sets):
+            one()
+        ctx.synchronize()
+        us = float(np.median([ev.time_ms(st, lambda: [one() for _ in range(reps)]) / reps for _ in range(5)])) * 1e3
+        nbytes = raw.nbytes + hidden * 4 + vocab * 4
+        out[name] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "weight_bytes": int(raw.nbytes),
+                     "copies": n_sets}
+        for w in ws:
+            w.free()
+    for _ in range(3):
+        ctx.argmax_dev(tok, y, vocab)
+    ctx.synchronize()
+    out["argmax_us"] = round(float(np.median([ev.time_ms(st, lambda: [ctx.argmax_dev(tok, y, vocab)
+                                                                      for _ in range(reps)]) / reps
+                                              for _ in range(5)])) * 1e3, 2)
+    for a in (x, y, tok):
+        a.free()
+    return out
+
+
 def cpu_gemv_baseline(seconds):
     """Oracle IQ2_XXS GEMV (dequantize + f32 GEMV, one thread), bounded sample:
     alternating [1536 x 2048] and [2048 x 1536] matrices for about `seconds`."""
@@ -415,6 +456,7 @@ def main():
                                   "batch 64 with Zipf(1.1) routing; cold: eight layers rotate (batch 1 also over "
                                   "61 tokens); warm: one layer, one input"}
     out["kv_q8_codec"] = kv_codec_section(ctx, ev, rng)
+    out["logits"] = logits_section(ctx, ev, rng)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_gemv_baseline(args.cpu_seconds)
         out["kv_q8_codec"]["cpu_quantize"] = cpu_kv_codec_baseline(rng)

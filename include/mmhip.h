@@ -145,6 +145,12 @@ int mmhip_dequantize(mmhip_ctx* ctx, float* out_host, const void* data_host,
  * the subnormal value truncated toward zero. A NaN value quantises to 0. */
 int mmhip_quantize_q8_0(mmhip_ctx* ctx, void* blocks_host, const float* x_host,
                         uint64_t n_elements);
+/* sampleGreedy (inference.zig:376-386) over n logits (computeLogits'
+ * output, inference.zig:1189-1197): *out_host = the first index of the
+ * largest logit (strict >, so ties keep the earlier index; a NaN never
+ * wins; a NaN logits[0] gives 0). 1 <= n < 2^32. */
+int mmhip_sample_greedy(mmhip_ctx* ctx, uint32_t* out_host, const float* logits_host,
+                        uint64_t n);
 /* Drop the resident copy keyed by ptr_host (all types/shapes). */
 int mmhip_forget(mmhip_ctx* ctx, const void* ptr_host);
 
@@ -166,6 +172,10 @@ int mmhip_quantize_q8_0_rows_dev(mmhip_ctx* ctx, void* blocks_dev, const float* 
  * blocks_dev must be 2-byte aligned. */
 int mmhip_dequantize_q8_0_rows_dev(mmhip_ctx* ctx, float* out_dev, uint64_t out_stride,
                                    const void* blocks_dev, uint64_t n_rows, uint32_t row_len);
+/* mmhip_sample_greedy on device logits; *out_dev receives the token id. The
+ * logits come from mmhip_gemv_dev with the output projection weight
+ * (computeLogits: hidden -> vocab_size). */
+int mmhip_argmax_dev(mmhip_ctx* ctx, uint32_t* out_dev, const float* logits_dev, uint64_t n);
 /* y[rows] = W[mat] . x[cols] for one matrix of a weight. */
 int mmhip_gemv_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat,
                    const float* x_dev, float* y_dev);

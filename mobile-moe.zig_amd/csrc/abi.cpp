@@ -113,6 +113,7 @@ void mmhip_destroy(mmhip_ctx* ctx) {
     ctx->d_out.release();
     ctx->d_raw.release();
     ctx->d_q.release();
+    ctx->d_arg.release();
     ctx->h_in.release();
     ctx->h_out.release();
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -368,6 +369,38 @@ int mmhip_quantize_q8_0(mmhip_ctx* ctx, void* blocks_host, const float* x_host, 
     if (e == hipSuccess) e = hipMemcpyAsync(blocks_host, ctx->d_raw.p, out_bytes, hipMemcpyDeviceToHost, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     return e == hipSuccess ? MMHIP_OK : hip_fail(e, "quantize_q8_0");
+}
+
+int mmhip_argmax_dev(mmhip_ctx* ctx, uint32_t* out_dev, const float* logits_dev, uint64_t n) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!out_dev || !logits_dev || n == 0 || n > 0xFFFFFFFFull) {
+        set_error(MMHIP_ERR_INVALID, "argmax_dev: null pointer or n outside [1, 2^32)");
+        return MMHIP_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipError_t e = ctx->d_arg.ensure(argmax_scratch_bytes(n));
+    if (e == hipSuccess) e = launch_argmax(logits_dev, n, out_dev, ctx->d_arg.p, ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "argmax_dev");
+}
+
+int mmhip_sample_greedy(mmhip_ctx* ctx, uint32_t* out_host, const float* logits_host, uint64_t n) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!out_host || !logits_host || n == 0 || n > 0xFFFFFFFFull) {
+        set_error(MMHIP_ERR_INVALID, "sample_greedy: null pointer or n outside [1, 2^32)");
+        return MMHIP_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipError_t e = ctx->d_out.ensure(n * 4);
+    if (e == hipSuccess) e = ctx->d_raw.ensure(4);
+    if (e == hipSuccess) e = ctx->d_arg.ensure(argmax_scratch_bytes(n));
+    if (e != hipSuccess) return hip_fail(e, "sample_greedy: scratch");
+    e = hipMemcpyAsync(ctx->d_out.p, logits_host, n * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = launch_argmax(static_cast<const float*>(ctx->d_out.p), n, static_cast<uint32_t*>(ctx->d_raw.p),
+                          ctx->d_arg.p, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out_host, ctx->d_raw.p, 4, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "sample_greedy");
 }
 
 int mmhip_gemv_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x_dev, float* y_dev) {

@@ -79,6 +79,7 @@ struct mmhip_ctx {
     std::mutex mu;                   // seam calls: scratch + residency map
     std::map<std::tuple<const void*, uint32_t, uint64_t, uint64_t>, mmhip_weight*> resident;
     mmhip::DevBuf d_in, d_out, d_raw, d_q;
+    mmhip::DevBuf d_arg;  // argmax partials (value, index) of the first pass
     mmhip::HostBuf h_in, h_out;
     KernelTimer timer;
 };

@@ -111,6 +111,12 @@ hipError_t launch_quantize_q8_0_rows(const float* x, uint64_t x_stride, uint64_t
 hipError_t launch_dequantize_q8_0_rows(const void* blocks, uint64_t n_rows, uint32_t row_len, float* out,
                                        uint64_t out_stride, hipStream_t s);
 
+// sampleGreedy (inference.zig:376-386): *out = the first index of the
+// largest of n logits (a NaN never wins; a NaN x[0] gives 0). 1 <= n < 2^32;
+// scratch holds argmax_scratch_bytes(n) bytes of device memory.
+uint64_t argmax_scratch_bytes(uint64_t n);
+hipError_t launch_argmax(const float* x, uint64_t n, uint32_t* out, void* scratch, hipStream_t s);
+
 // Raw GGUF bytes -> tile layout.
 hipError_t launch_repack(const void* raw, const TileGeom& g, uint4* recs, uint16_t* dvals, hipStream_t s);
 

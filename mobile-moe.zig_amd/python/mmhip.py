@@ -97,6 +97,8 @@ _SIGS = {
     "mmhip_forget": (ctypes.c_int, [_c_void_p, _c_void_p]),
     "mmhip_dequantize_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u32, _u64]),
     "mmhip_quantize_q8_0": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u64]),
+    "mmhip_sample_greedy": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u64]),
+    "mmhip_argmax_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u64]),
     "mmhip_quantize_q8_0_rows_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u64, _u64, _u32]),
     "mmhip_dequantize_q8_0_rows_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _u64, _u32]),
     "mmhip_gemv_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _c_void_p]),
@@ -298,6 +300,16 @@ class Context:
         out = np.empty(((x.size + 31) // 32) * 34, dtype=np.uint8)
         check(self.lib.mmhip_quantize_q8_0(self.handle, _ptr(out), _ptr(x), x.size), "mmhip_quantize_q8_0")
         return out
+
+    def sample_greedy(self, logits: np.ndarray) -> int:
+        """sampleGreedy (inference.zig:376-386) on the device."""
+        logits = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+        out = np.zeros(1, dtype=np.uint32)
+        check(self.lib.mmhip_sample_greedy(self.handle, _ptr(out), _ptr(logits), logits.size), "mmhip_sample_greedy")
+        return int(out[0])
+
+    def argmax_dev(self, out: "DeviceArray", logits: "DeviceArray", n: int, out_offset: int = 0):
+        check(self.lib.mmhip_argmax_dev(self.handle, out.ptr + out_offset, logits.ptr, n), "mmhip_argmax_dev")
 
     def forget(self, raw: np.ndarray):
         check(self.lib.mmhip_forget(self.handle, _ptr(raw)), "mmhip_forget")

@@ -101,6 +101,8 @@ extern fn mmhip_mat_vec_mul(ctx: *Ctx, out_host: [*]f32, ptr_host: ?*const anyop
 extern fn mmhip_batch_mat_mul(ctx: *Ctx, out_host: [*]f32, ptr_host: ?*const anyopaque, type_: u32, in_host: [*]const f32, out_dim: u64, batch: u64, in_dim: u64) c_int;
 extern fn mmhip_dequantize(ctx: *Ctx, out_host: [*]f32, data_host: ?*const anyopaque, type_: u32, n_elements: u64) c_int;
 extern fn mmhip_forget(ctx: *Ctx, ptr_host: ?*const anyopaque) c_int;
+extern fn mmhip_sample_greedy(ctx: *Ctx, out_host: *u32, logits_host: [*]const f32, n: u64) c_int;
+extern fn mmhip_argmax_dev(ctx: *Ctx, out_dev: ?*anyopaque, logits_dev: ?*const anyopaque, n: u64) c_int;
 extern fn mmhip_quantize_q8_0(ctx: *Ctx, blocks_host: ?*anyopaque, x_host: [*]const f32, n_elements: u64) c_int;
 extern fn mmhip_quantize_q8_0_rows_dev(ctx: *Ctx, blocks_dev: ?*anyopaque, x_dev: ?*const anyopaque, x_stride: u64, n_rows: u64, row_len: u32) c_int;
 extern fn mmhip_dequantize_q8_0_rows_dev(ctx: *Ctx, out_dev: ?*anyopaque, out_stride: u64, blocks_dev: ?*const anyopaque, n_rows: u64, row_len: u32) c_int;
@@ -192,6 +194,20 @@ pub const HipBackend = struct {
     /// dequant.dequantize (dequant.zig:632-659) on the device, bit-exact.
     pub fn dequantize(self: *Self, out: []f32, data: [*]const u8, type_: gguf.GgmlType) !void {
         try check(mmhip_dequantize(self.ctx, out.ptr, data, @intFromEnum(type_), out.len));
+    }
+
+    /// Engine.sampleGreedy (inference.zig:376-386) on the device: the first
+    /// index of the largest logit.
+    pub fn sampleGreedy(self: *Self, logits: []const f32) !u32 {
+        var id: u32 = 0;
+        try check(mmhip_sample_greedy(self.ctx, &id, logits.ptr, logits.len));
+        return id;
+    }
+
+    /// sampleGreedy on device logits (e.g. computeLogits' GEMV output kept
+    /// on the device); the id lands in device memory.
+    pub fn argmaxDev(self: *Self, out_dev: *anyopaque, logits_dev: *const anyopaque, n: u64) !void {
+        try check(mmhip_argmax_dev(self.ctx, out_dev, logits_dev, n));
     }
 
     /// dequant.quantizeQ8_0 (dequant.zig:98-130) on the device: `blocks`

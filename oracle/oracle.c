@@ -155,6 +155,20 @@ void orc_dequantize_q8_0_rows(const uint8_t* blocks, uint64_t n_rows, uint32_t r
     for (uint64_t r = 0; r < n_rows; ++r) orc_dequantize_q8_0(blocks + r * rb, row_len, out + r * row_len);
 }
 
+/* sampleGreedy, inference.zig:376-386: best = logits[0]; for i >= 1, a
+ * strictly greater logit takes over (ties keep the earlier index, a NaN
+ * never takes over, a NaN logits[0] is never displaced). n >= 1. */
+uint32_t orc_sample_greedy(const float* logits, uint64_t n) {
+    uint32_t best_id = 0;
+    float best = logits[0];
+    for (uint64_t i = 1; i < n; ++i)
+        if (logits[i] > best) {
+            best = logits[i];
+            best_id = (uint32_t)i;
+        }
+    return best_id;
+}
+
 /* GgmlType.blockSize / blockBytes / tensorBytes, gguf.zig:59-117 (the types
  * on this path). */
 uint64_t orc_block_size(uint32_t type) {

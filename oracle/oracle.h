@@ -21,6 +21,9 @@
  *                           reference defect (see the function) and is only
  *                           checked to report it.
  *   orc_dequantize_q8_0     closed form d*q (exact in f32) on all 65,536 d codes.
+ *   orc_sample_greedy       numpy argmax (first occurrence) on NaN-free data,
+ *                           hand-derived cases: ties, -0 vs +0, NaN at 0 and
+ *                           elsewhere, all equal, -inf.
  *   orc_quantize_q8_0       reference KAT kv_cache.zig:686-719 (put/get round
  *                           trip within 5% + 1e-2), stored d = f32ToF16(max/127)
  *                           (normal range: the pinned converter; subnormal:
@@ -72,6 +75,7 @@ uint64_t orc_iq2xxs_grid(uint32_t idx);
 uint8_t orc_ksigns(uint32_t code);
 void orc_dequantize_q8_0(const uint8_t* data, uint64_t n_elements, float* out);
 void orc_quantize_q8_0(const float* x, uint64_t n_elements, uint8_t* out);
+uint32_t orc_sample_greedy(const float* logits, uint64_t n);
 void orc_quantize_q8_0_rows(const float* x, uint64_t x_stride, uint64_t n_rows, uint32_t row_len, uint8_t* out);
 void orc_dequantize_q8_0_rows(const uint8_t* blocks, uint64_t n_rows, uint32_t row_len, float* out);
 void orc_dequantize_iq2xxs_block(const uint8_t* block, float* out256);

@@ -47,6 +47,7 @@ _SIGS = {
     "orc_ksigns": (ctypes.c_uint8, [_u32]),
     "orc_dequantize_q8_0": (None, [_vp, _u64, _vp]),
     "orc_quantize_q8_0": (None, [_vp, _u64, _vp]),
+    "orc_sample_greedy": (_u32, [_vp, _u64]),
     "orc_quantize_q8_0_rows": (None, [_vp, _u64, _u64, _u32, _vp]),
     "orc_dequantize_q8_0_rows": (None, [_vp, _u64, _u32, _vp]),
     "orc_dequantize_iq2xxs_block": (None, [_vp, _vp]),
@@ -99,6 +100,12 @@ def f32_to_f16(v: float):
     d = ctypes.c_int(0)
     r = lib().orc_f32_to_f16(v, ctypes.byref(d))
     return r, bool(d.value)
+
+
+def sample_greedy(logits: np.ndarray) -> int:
+    """sampleGreedy (inference.zig:376-386)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+    return int(lib().orc_sample_greedy(_p(logits), logits.size))
 
 
 def quantize_q8_0(x: np.ndarray) -> np.ndarray:

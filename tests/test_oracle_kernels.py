@@ -249,3 +249,24 @@ def test_moe_ffn_pool_matches_serial(orc):
         pool.close()
     b, ib, wb = moe.ffn(h)
     assert np.array_equal(a, b) and np.array_equal(ia, ib) and np.array_equal(wa, wb)
+
+
+# ---- sampleGreedy (inference.zig:376-386) ----
+
+def test_sample_greedy_cases(orc):
+    f = np.float32
+    assert orc.sample_greedy(np.array([1, 3, 3, 2], f)) == 1          # ties keep the earlier index
+    assert orc.sample_greedy(np.array([-0.0, 0.0], f)) == 0           # -0 == +0: no takeover
+    assert orc.sample_greedy(np.array([0.0, -0.0], f)) == 0
+    assert orc.sample_greedy(np.array([np.nan, 5, 9], f)) == 0        # a NaN logits[0] stays
+    assert orc.sample_greedy(np.array([1, np.nan, 0.5, 2, np.nan], f)) == 3  # NaN never takes over
+    assert orc.sample_greedy(np.array([-np.inf, np.nan, -np.inf], f)) == 0
+    assert orc.sample_greedy(np.full(7, 2.5, f)) == 0
+    assert orc.sample_greedy(np.array([4.0], f)) == 0
+
+
+def test_sample_greedy_matches_numpy_first_argmax(orc):
+    rng = np.random.default_rng(11)
+    for n in (2, 17, 1000, 154880):
+        x = rng.integers(-50, 50, n).astype(np.float32)  # many ties
+        assert orc.sample_greedy(x) == int(np.argmax(x))

@@ -94,3 +94,4 @@ def test_subnormal_scale_truncates(orc):
     d = np.float32(np.float32(1e-4) / np.float32(127.0))
     assert d16[0] == int(np.floor(float(d) / 2.0 ** -24))
     assert qs[0, 5] == 127 and qs[0, 6] == int(_nearest_away(float(np.float32(np.float32(-3e-5) / d))))
+
