@@ -44,6 +44,7 @@ extern "C" {
 #define MMHIP_ERR_UNSUPPORTED (-3) /* tensor type not on this path */
 #define MMHIP_ERR_HIP (-4)         /* HIP runtime error (see last error) */
 #define MMHIP_ERR_NOMEM (-5)
+#define MMHIP_ERR_NOT_FOUND (-6) /* GGUF tensor or metadata key absent, or of another type */
 
 /* ---- GgmlType ids (src/gguf.zig:21-56) ---- */
 #define MMHIP_TYPE_F32 0u
@@ -116,6 +117,68 @@ int mmhip_weight_from_device(mmhip_ctx* ctx, const void* raw_dev, uint32_t type,
 void mmhip_weight_free(mmhip_ctx* ctx, mmhip_weight* w);
 /* Device bytes held by the weight (tile records + scales). */
 uint64_t mmhip_weight_device_bytes(const mmhip_weight* w);
+
+/* ======================================================================
+ * GGUF v3 files and device-resident weights from them. These replace
+ *   gguf.loadFromFile / parse (src/gguf.zig:266-413): the file is mapped
+ *     read-only (MAP_PRIVATE + MADV_WILLNEED) and parsed; errors carry the
+ *     reference's names (InvalidMagic, UnsupportedVersion, StringTooLong,
+ *     ArrayTooLong, TooManyDimensions, UnsupportedMetadataType,
+ *     UnsupportedArrayType, EndOfStream) in mmhip_last_error();
+ *   GgufFile.tensor_infos.get + tensorPtr (src/gguf.zig:218-229);
+ *   GgufFile.metaString / metaInt / metaFloat (src/gguf.zig:232-262);
+ *   Model.bindTensor / bindLayer's FFN tensors (src/model.zig:261-395) with
+ *     a one-time upload into the tile layout the kernels read.
+ * A tensor's dims[0] is its row length (ggml order): a matrix stack is
+ * [cols, rows, count]. Pointers returned stay valid until mmhip_gguf_close.
+ * ====================================================================== */
+
+typedef struct mmhip_gguf mmhip_gguf;
+typedef struct {
+    uint32_t version;            /* 3 */
+    uint64_t tensor_count;       /* header counts */
+    uint64_t metadata_count;
+    uint64_t n_tensors, n_keys;  /* distinct names / keys */
+    uint64_t alignment;          /* general.alignment or 32 */
+    uint64_t data_offset;        /* start of the tensor data section */
+    uint64_t file_size;
+} mmhip_gguf_info;
+typedef struct {                 /* TensorInfo (src/gguf.zig:162-175) */
+    const char* name;
+    uint32_t n_dims;
+    uint64_t dims[4];            /* unused dimensions are 1 */
+    uint32_t type;               /* GgmlType */
+    uint64_t offset;             /* from data_offset */
+    uint64_t n_elements;         /* TensorInfo.nElements */
+    uint64_t n_bytes;            /* GgmlType.tensorBytes; 0 for a type this library does not read */
+    const void* data;            /* mapped bytes, NULL if the type is not read here or they leave the file */
+} mmhip_gguf_tensor;
+
+int mmhip_gguf_open(const char* path, mmhip_gguf** out);
+void mmhip_gguf_close(mmhip_gguf* g);
+int mmhip_gguf_get_info(const mmhip_gguf* g, mmhip_gguf_info* out);
+/* Tensors and keys in file order (first occurrence of a repeated name). */
+int mmhip_gguf_tensor_at(const mmhip_gguf* g, uint64_t index, mmhip_gguf_tensor* out);
+int mmhip_gguf_find_tensor(const mmhip_gguf* g, const char* name, mmhip_gguf_tensor* out);
+const char* mmhip_gguf_key_at(const mmhip_gguf* g, uint64_t index);
+/* Metadata value type (MetadataValueType, src/gguf.zig:121-135) or < 0. */
+int mmhip_gguf_meta_type(const mmhip_gguf* g, const char* key);
+int mmhip_gguf_meta_int(const mmhip_gguf* g, const char* key, int64_t* out);
+int mmhip_gguf_meta_float(const mmhip_gguf* g, const char* key, double* out);
+/* Not NUL-terminated: *len bytes. */
+int mmhip_gguf_meta_string(const mmhip_gguf* g, const char* key, const char** str, uint64_t* len);
+/* Numeric arrays: len little-endian elements; string arrays: len records of
+ * [u64 length][bytes] (the layout MetadataArray.data holds). */
+int mmhip_gguf_meta_array(const mmhip_gguf* g, const char* key, uint32_t* elem_type, uint64_t* len,
+                          const void** data, uint64_t* n_bytes);
+/* mmhip_weight_upload of the named tensor (rows = dims[1], cols = dims[0],
+ * count = dims[2]). */
+int mmhip_weight_upload_gguf(mmhip_ctx* ctx, const mmhip_gguf* g, const char* name, mmhip_weight** out_w);
+/* mmhip_moe_layer_create from blk.<layer>.ffn_gate_inp / ffn_{gate,up,down}_exps
+ * and, when present, ffn_{gate,up,down}_shexp; routed_scaling_factor from
+ * <general.architecture>.expert_weights_scale (default 1). */
+int mmhip_moe_layer_create_gguf(mmhip_ctx* ctx, const mmhip_gguf* g, uint32_t layer,
+                                mmhip_moe_layer** out_layer);
 
 /* ======================================================================
  * Engine seam, host slices. These replace the bodies of

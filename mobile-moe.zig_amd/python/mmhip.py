@@ -67,6 +67,16 @@ class PerfEntry(ctypes.Structure):
 
 
 # name -> (restype, argtypes)
+class GgufInfo(ctypes.Structure):
+    _fields_ = [("version", _u32), ("tensor_count", _u64), ("metadata_count", _u64), ("n_tensors", _u64),
+                ("n_keys", _u64), ("alignment", _u64), ("data_offset", _u64), ("file_size", _u64)]
+
+
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("n_dims", _u32), ("dims", _u64 * 4), ("type", _u32), ("offset", _u64),
+                ("n_elements", _u64), ("n_bytes", _u64), ("data", _c_void_p)]
+
+
 _SIGS = {
     "mmhip_last_error": (ctypes.c_char_p, []),
     "mmhip_is_available": (ctypes.c_int, []),
@@ -112,6 +122,21 @@ _SIGS = {
     "mmhip_moe_ffn_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _u32,
                                          ctypes.POINTER(RouteParams), _c_void_p, _c_void_p]),
     "mmhip_moe_expert_counts": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p]),
+    "mmhip_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_c_void_p)]),
+    "mmhip_gguf_close": (None, [_c_void_p]),
+    "mmhip_gguf_get_info": (ctypes.c_int, [_c_void_p, ctypes.POINTER(GgufInfo)]),
+    "mmhip_gguf_tensor_at": (ctypes.c_int, [_c_void_p, _u64, ctypes.POINTER(GgufTensor)]),
+    "mmhip_gguf_find_tensor": (ctypes.c_int, [_c_void_p, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]),
+    "mmhip_gguf_key_at": (ctypes.c_char_p, [_c_void_p, _u64]),
+    "mmhip_gguf_meta_type": (ctypes.c_int, [_c_void_p, ctypes.c_char_p]),
+    "mmhip_gguf_meta_int": (ctypes.c_int, [_c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "mmhip_gguf_meta_float": (ctypes.c_int, [_c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "mmhip_gguf_meta_string": (ctypes.c_int, [_c_void_p, ctypes.c_char_p, ctypes.POINTER(_c_void_p),
+                                              ctypes.POINTER(_u64)]),
+    "mmhip_gguf_meta_array": (ctypes.c_int, [_c_void_p, ctypes.c_char_p, ctypes.POINTER(_u32), ctypes.POINTER(_u64),
+                                             ctypes.POINTER(_c_void_p), ctypes.POINTER(_u64)]),
+    "mmhip_weight_upload_gguf": (ctypes.c_int, [_c_void_p, _c_void_p, ctypes.c_char_p, ctypes.POINTER(_c_void_p)]),
+    "mmhip_moe_layer_create_gguf": (ctypes.c_int, [_c_void_p, _c_void_p, _u32, ctypes.POINTER(_c_void_p)]),
     "mmhip_plan_layer": (ctypes.c_int, [_u32, ctypes.POINTER(PlanHParams), ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.POINTER(PerfEntry), ctypes.c_size_t,
                                         ctypes.POINTER(OpSchedule), ctypes.c_size_t,
@@ -254,6 +279,17 @@ class Context:
               "mmhip_weight_upload")
         return Weight(self, h.value, ggml_type, rows, cols, count)
 
+    def upload_gguf(self, g: "Gguf", name: str) -> Weight:
+        """One-time upload of a GGUF tensor (rows = dims[1], cols = dims[0], count = dims[2])."""
+        t = g.tensor(name)
+        if t is None:
+            raise KeyError(name)
+        h = _c_void_p()
+        check(self.lib.mmhip_weight_upload_gguf(self.handle, g.handle, name.encode(), ctypes.byref(h)),
+              "mmhip_weight_upload_gguf")
+        d = t["dims"]
+        return Weight(self, h.value, t["type"], d[1], d[0], d[2])
+
     def weight_from_device(self, raw: DeviceArray, ggml_type: int, rows: int, cols: int, count: int = 1) -> Weight:
         h = _c_void_p()
         check(self.lib.mmhip_weight_from_device(self.handle, raw.ptr, ggml_type, rows, cols, count,
@@ -340,6 +376,97 @@ class Context:
               "mmhip_dequantize_q8_0_rows_dev")
 
 
+class Gguf:
+    """A memory-mapped GGUF v3 file (gguf.loadFromFile / parse, gguf.zig:266-413)."""
+
+    NOT_FOUND = -6
+
+    def __init__(self, path):
+        self.lib = load_library()
+        h = _c_void_p()
+        check(self.lib.mmhip_gguf_open(os.fsencode(path), ctypes.byref(h)), "mmhip_gguf_open")
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            self.lib.mmhip_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self) -> dict:
+        i = GgufInfo()
+        check(self.lib.mmhip_gguf_get_info(self.handle, ctypes.byref(i)), "mmhip_gguf_get_info")
+        return {f: getattr(i, f) for f, _ in GgufInfo._fields_}
+
+    @staticmethod
+    def _tensor_dict(t: GgufTensor) -> dict:
+        return dict(name=t.name.decode(), n_dims=t.n_dims, dims=tuple(t.dims), type=t.type, offset=t.offset,
+                    n_elements=t.n_elements, n_bytes=t.n_bytes, data=t.data)
+
+    def tensors(self) -> list:
+        out = []
+        for i in range(self.info()["n_tensors"]):
+            t = GgufTensor()
+            check(self.lib.mmhip_gguf_tensor_at(self.handle, i, ctypes.byref(t)), "mmhip_gguf_tensor_at")
+            out.append(self._tensor_dict(t))
+        return out
+
+    def tensor(self, name: str) -> Optional[dict]:
+        t = GgufTensor()
+        rc = self.lib.mmhip_gguf_find_tensor(self.handle, name.encode(), ctypes.byref(t))
+        if rc == self.NOT_FOUND:
+            return None
+        check(rc, "mmhip_gguf_find_tensor")
+        return self._tensor_dict(t)
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        """A copy of the tensor's mapped bytes."""
+        t = self.tensor(name)
+        if t is None or not t["data"]:
+            raise KeyError(name)
+        return np.ctypeslib.as_array(ctypes.cast(t["data"], ctypes.POINTER(ctypes.c_uint8)), (t["n_bytes"],)).copy()
+
+    def keys(self) -> list:
+        return [self.lib.mmhip_gguf_key_at(self.handle, i).decode() for i in range(self.info()["n_keys"])]
+
+    def meta_type(self, key: str) -> Optional[int]:
+        rc = self.lib.mmhip_gguf_meta_type(self.handle, key.encode())
+        return None if rc < 0 else rc
+
+    def meta_int(self, key: str) -> Optional[int]:
+        v = ctypes.c_int64()
+        rc = self.lib.mmhip_gguf_meta_int(self.handle, key.encode(), ctypes.byref(v))
+        return None if rc == self.NOT_FOUND else (check(rc, "mmhip_gguf_meta_int"), v.value)[1]
+
+    def meta_float(self, key: str) -> Optional[float]:
+        v = ctypes.c_double()
+        rc = self.lib.mmhip_gguf_meta_float(self.handle, key.encode(), ctypes.byref(v))
+        return None if rc == self.NOT_FOUND else (check(rc, "mmhip_gguf_meta_float"), v.value)[1]
+
+    def meta_string(self, key: str) -> Optional[bytes]:
+        p, n = _c_void_p(), _u64()
+        rc = self.lib.mmhip_gguf_meta_string(self.handle, key.encode(), ctypes.byref(p), ctypes.byref(n))
+        if rc == self.NOT_FOUND:
+            return None
+        check(rc, "mmhip_gguf_meta_string")
+        return ctypes.string_at(p.value, n.value) if n.value else b""
+
+    def meta_array(self, key: str) -> Optional[tuple]:
+        """(element type, length, payload bytes)."""
+        et, n, p, nb = _u32(), _u64(), _c_void_p(), _u64()
+        rc = self.lib.mmhip_gguf_meta_array(self.handle, key.encode(), ctypes.byref(et), ctypes.byref(n),
+                                            ctypes.byref(p), ctypes.byref(nb))
+        if rc == self.NOT_FOUND:
+            return None
+        check(rc, "mmhip_gguf_meta_array")
+        return et.value, n.value, (ctypes.string_at(p.value, nb.value) if nb.value else b"")
+
+
 class MoeLayer:
     """Device-resident MoE FFN layer (moeFFN + Scheduler.route on the GPU)."""
 
@@ -364,6 +491,21 @@ class MoeLayer:
         h = _c_void_p()
         check(ctx.lib.mmhip_moe_layer_create(ctx.handle, ctypes.byref(w), ctypes.byref(h)), "mmhip_moe_layer_create")
         self.handle = h.value
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, g: "Gguf", layer: int) -> "MoeLayer":
+        """Model.bindLayer's FFN tensors (model.zig:289-395) of blk.<layer>, uploaded once."""
+        gate = g.tensor(f"blk.{layer}.ffn_gate_exps.weight")
+        if gate is None:
+            raise KeyError(f"blk.{layer}.ffn_gate_exps.weight")
+        self = cls.__new__(cls)
+        self.ctx, self._keep = ctx, [g]
+        self.hidden, self.inter, self.n_experts = gate["dims"][0], gate["dims"][1], gate["dims"][2]
+        h = _c_void_p()
+        check(ctx.lib.mmhip_moe_layer_create_gguf(ctx.handle, g.handle, layer, ctypes.byref(h)),
+              "mmhip_moe_layer_create_gguf")
+        self.handle = h.value
+        return self
 
     def free(self):
         if self.handle:

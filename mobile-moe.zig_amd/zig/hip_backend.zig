@@ -20,6 +20,7 @@ const dequant = @import("dequant.zig");
 pub const Ctx = opaque {};
 pub const Weight = opaque {};
 pub const MoeLayerHandle = opaque {};
+pub const GgufHandle = opaque {};
 
 pub const MoeWeights = extern struct {
     hidden_size: u32,
@@ -75,6 +76,28 @@ pub const PerfEntry = extern struct {
     gpu_us: u64,
 };
 
+pub const GgufInfo = extern struct {
+    version: u32 = 0,
+    tensor_count: u64 = 0,
+    metadata_count: u64 = 0,
+    n_tensors: u64 = 0,
+    n_keys: u64 = 0,
+    alignment: u64 = 0,
+    data_offset: u64 = 0,
+    file_size: u64 = 0,
+};
+
+pub const GgufTensor = extern struct {
+    name: ?[*:0]const u8 = null,
+    n_dims: u32 = 0,
+    dims: [4]u64 = .{ 1, 1, 1, 1 },
+    type_: u32 = 0,
+    offset: u64 = 0,
+    n_elements: u64 = 0,
+    n_bytes: u64 = 0,
+    data: ?*const anyopaque = null,
+};
+
 pub const max_moe_tokens: u32 = 256;
 
 extern fn mmhip_last_error() [*:0]const u8;
@@ -93,6 +116,19 @@ extern fn mmhip_free(ctx: *Ctx, dev: ?*anyopaque) c_int;
 extern fn mmhip_memcpy_h2d(ctx: *Ctx, dst_dev: ?*anyopaque, src_host: ?*const anyopaque, bytes: usize) c_int;
 extern fn mmhip_memcpy_d2h(ctx: *Ctx, dst_host: ?*anyopaque, src_dev: ?*const anyopaque, bytes: usize) c_int;
 extern fn mmhip_memset_dev(ctx: *Ctx, dst_dev: ?*anyopaque, value: c_int, bytes: usize) c_int;
+extern fn mmhip_gguf_open(path: [*:0]const u8, out: *?*GgufHandle) c_int;
+extern fn mmhip_gguf_close(g: ?*GgufHandle) void;
+extern fn mmhip_gguf_get_info(g: *const GgufHandle, out: *GgufInfo) c_int;
+extern fn mmhip_gguf_tensor_at(g: *const GgufHandle, index: u64, out: *GgufTensor) c_int;
+extern fn mmhip_gguf_find_tensor(g: *const GgufHandle, name: [*:0]const u8, out: *GgufTensor) c_int;
+extern fn mmhip_gguf_key_at(g: *const GgufHandle, index: u64) ?[*:0]const u8;
+extern fn mmhip_gguf_meta_type(g: *const GgufHandle, key: [*:0]const u8) c_int;
+extern fn mmhip_gguf_meta_int(g: *const GgufHandle, key: [*:0]const u8, out: *i64) c_int;
+extern fn mmhip_gguf_meta_float(g: *const GgufHandle, key: [*:0]const u8, out: *f64) c_int;
+extern fn mmhip_gguf_meta_string(g: *const GgufHandle, key: [*:0]const u8, str: *?[*]const u8, len: *u64) c_int;
+extern fn mmhip_gguf_meta_array(g: *const GgufHandle, key: [*:0]const u8, elem_type: *u32, len: *u64, data: *?*const anyopaque, n_bytes: *u64) c_int;
+extern fn mmhip_weight_upload_gguf(ctx: *Ctx, g: *const GgufHandle, name: [*:0]const u8, out_w: *?*Weight) c_int;
+extern fn mmhip_moe_layer_create_gguf(ctx: *Ctx, g: *const GgufHandle, layer: u32, out_layer: *?*MoeLayerHandle) c_int;
 extern fn mmhip_weight_upload(ctx: *Ctx, raw_host: ?*const anyopaque, type_: u32, rows: u64, cols: u64, count: u64, out_w: *?*Weight) c_int;
 extern fn mmhip_weight_from_device(ctx: *Ctx, raw_dev: ?*const anyopaque, type_: u32, rows: u64, cols: u64, count: u64, out_w: *?*Weight) c_int;
 extern fn mmhip_weight_free(ctx: *Ctx, w: ?*Weight) void;
@@ -127,6 +163,7 @@ pub const HipError = error{
     HipUnsupportedType,
     HipLaunch,
     HipOutOfMemory,
+    HipNotFound,
 };
 
 fn check(rc: c_int) HipError!void {
@@ -137,6 +174,7 @@ fn check(rc: c_int) HipError!void {
         -2 => error.HipInvalidArgument,
         -3 => error.HipUnsupportedType,
         -5 => error.HipOutOfMemory,
+        -6 => error.HipNotFound,
         else => error.HipLaunch,
     };
 }
@@ -254,6 +292,15 @@ pub const MoeLayer = struct {
         return .{ .backend = backend, .handle = h.?, .hidden = w.hidden_size };
     }
 
+    /// The same from blk.<layer>'s FFN tensors of a GGUF file opened by
+    /// GgufFile.open (Model.bindLayer, model.zig:289-395); the file may be
+    /// closed afterwards.
+    pub fn fromGguf(backend: *HipBackend, file: *const GgufFile, layer: u32, hidden: u32) !MoeLayer {
+        var h: ?*MoeLayerHandle = null;
+        try check(mmhip_moe_layer_create_gguf(backend.ctx, file.handle, layer, &h));
+        return .{ .backend = backend, .handle = h.?, .hidden = hidden };
+    }
+
     pub fn destroy(self: *MoeLayer) void {
         mmhip_moe_layer_destroy(self.backend.ctx, self.handle);
     }
@@ -278,6 +325,87 @@ pub const MoeLayer = struct {
 
 /// Plans one layer (RMSNorm, attention, RMSNorm, FFN); `out` receives the
 /// ops. Returns the number written.
+/// A GGUF v3 file mapped and parsed by libmmhip (gguf.loadFromFile,
+/// gguf.zig:368-413), for uploading tensors by name.
+pub const GgufFile = struct {
+    handle: *GgufHandle,
+
+    pub fn open(path: [*:0]const u8) !GgufFile {
+        var h: ?*GgufHandle = null;
+        try check(mmhip_gguf_open(path, &h));
+        return .{ .handle = h.? };
+    }
+
+    pub fn close(self: *GgufFile) void {
+        mmhip_gguf_close(self.handle);
+    }
+
+    pub fn info(self: *const GgufFile) !GgufInfo {
+        var i = GgufInfo{};
+        try check(mmhip_gguf_get_info(self.handle, &i));
+        return i;
+    }
+
+    pub fn tensorAt(self: *const GgufFile, index: u64) !GgufTensor {
+        var t = GgufTensor{};
+        try check(mmhip_gguf_tensor_at(self.handle, index, &t));
+        return t;
+    }
+
+    pub fn keyAt(self: *const GgufFile, index: u64) ?[*:0]const u8 {
+        return mmhip_gguf_key_at(self.handle, index);
+    }
+
+    /// tensor_infos.get + tensorPtr (gguf.zig:218-229); null if absent.
+    pub fn findTensor(self: *const GgufFile, name: [*:0]const u8) ?GgufTensor {
+        var t = GgufTensor{};
+        if (mmhip_gguf_find_tensor(self.handle, name, &t) != 0) return null;
+        return t;
+    }
+
+    /// metaInt / metaFloat / metaString (gguf.zig:232-262); null if absent or of another type.
+    pub fn metaInt(self: *const GgufFile, key: [*:0]const u8) ?i64 {
+        var v: i64 = 0;
+        return if (mmhip_gguf_meta_int(self.handle, key, &v) == 0) v else null;
+    }
+
+    pub fn metaFloat(self: *const GgufFile, key: [*:0]const u8) ?f64 {
+        var v: f64 = 0;
+        return if (mmhip_gguf_meta_float(self.handle, key, &v) == 0) v else null;
+    }
+
+    pub fn metaString(self: *const GgufFile, key: [*:0]const u8) ?[]const u8 {
+        var p: ?[*]const u8 = null;
+        var n: u64 = 0;
+        if (mmhip_gguf_meta_string(self.handle, key, &p, &n) != 0) return null;
+        return if (n == 0) "" else p.?[0..@intCast(n)];
+    }
+
+    /// Metadata value type (MetadataValueType), null if absent.
+    pub fn metaType(self: *const GgufFile, key: [*:0]const u8) ?u32 {
+        const t = mmhip_gguf_meta_type(self.handle, key);
+        return if (t < 0) null else @intCast(t);
+    }
+
+    /// Raw array payload: numeric elements little-endian, strings as [u64 len][bytes].
+    pub fn metaArray(self: *const GgufFile, key: [*:0]const u8) ?struct { elem_type: u32, len: u64, data: []const u8 } {
+        var et: u32 = 0;
+        var n: u64 = 0;
+        var d: ?*const anyopaque = null;
+        var nb: u64 = 0;
+        if (mmhip_gguf_meta_array(self.handle, key, &et, &n, &d, &nb) != 0) return null;
+        const bytes: []const u8 = if (nb == 0) "" else @as([*]const u8, @ptrCast(d.?))[0..@intCast(nb)];
+        return .{ .elem_type = et, .len = n, .data = bytes };
+    }
+
+    /// One-time device upload of a tensor ([cols, rows, count] in ggml order).
+    pub fn upload(self: *const GgufFile, backend: *HipBackend, name: [*:0]const u8) !*Weight {
+        var w: ?*Weight = null;
+        try check(mmhip_weight_upload_gguf(backend.ctx, self.handle, name, &w));
+        return w.?;
+    }
+};
+
 pub fn planLayer(layer: u32, hp: PlanHyperParams, has_gpu: bool, has_npu: bool, throttle_level: i32, db: []const PerfEntry, out: []OpSchedule) !usize {
     var n: usize = 0;
     try check(mmhip_plan_layer(layer, &hp, @intFromBool(has_gpu), @intFromBool(has_npu), throttle_level, if (db.len > 0) db.ptr else null, db.len, out.ptr, out.len, &n));
