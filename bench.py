@@ -298,6 +298,59 @@ def logits_section(ctx, ev, rng, reps=20, vocab=154880, hidden=HIDDEN):
     return out
 
 
+def mla_section(ctx, ev, rng, reps=20, n_layers=47, batch=64):
+    """MLA attention projections (inference.zig:467-489, 663-665; batch path
+    684-706, 880-882) on the same kernels: q_a [768 x 2048], q_b [3840 x 768],
+    kv_a [576 x 2048], o_proj [2048 x 2560], one layer's four GEMVs per decode
+    step with the weights of 47 layers rotating (cold, as in decode), and the
+    four batched products at 64 tokens."""
+    shapes = {"q_a": (768, 2048), "q_b": (3840, 768), "kv_a": (576, 2048), "o_proj": (2048, 2560)}
+    st = ctx.stream
+    xs = {n: mm.DeviceArray.from_numpy(ctx, rng.standard_normal(batch * c).astype(np.float32))
+          for n, (_, c) in shapes.items()}
+    ys = {n: mm.DeviceArray(ctx, batch * r * 4) for n, (r, _) in shapes.items()}
+    out = {"workload": f"MLA projections of {n_layers} layers: " +
+                       ", ".join(f"{n} [{r}x{c}]" for n, (r, c) in shapes.items()) +
+                       f"; decode = the four GEMVs of one layer, batch = the four products at {batch} tokens"}
+    for name, t in (("q8_0", mm.Q8_0), ("iq2_xxs", mm.IQ2_XXS)):
+        raws = {n: mm.make_weight(rng, t, r, c) for n, (r, c) in shapes.items()}
+        layers = [{n: ctx.upload(raws[n], t, r, c) for n, (r, c) in shapes.items()} for _ in range(n_layers)]
+        k = [0]
+
+        def decode():
+            lw = layers[k[0] % n_layers]
+            for n in shapes:
+                ctx.gemv_batched_dev(lw[n], 0, 1, xs[n], 0, ys[n], 0)
+            k[0] += 1
+
+        def prefill():
+            lw = layers[k[0] % n_layers]
+            for n in shapes:
+                ctx.qmm_dev(lw[n], 0, xs[n], ys[n], batch)
+            k[0] += 1
+
+        res = {}
+        for label, fn in (("decode", decode), ("batch64", prefill)):
+            for _ in range(n_layers):
+                fn()
+            ctx.synchronize()
+            us = float(np.median([ev.time_ms(st, lambda: [fn() for _ in range(reps)]) / reps
+                                  for _ in range(5)])) * 1e3
+            res[label + "_us_per_layer"] = round(us, 2)
+        wbytes = sum(int(r.nbytes) for r in raws.values())
+        nbytes = wbytes + sum(4 * (r + c) for r, c in shapes.values())
+        res["decode_GB/s"] = round(nbytes / (res["decode_us_per_layer"] * 1e-6) / 1e9, 1)
+        res["decode_frac"] = round(res["decode_GB/s"] / HBM_PEAK_GBS, 4)
+        res["weight_bytes_per_layer"] = wbytes
+        out[name] = res
+        for lw in layers:
+            for w in lw.values():
+                w.free()
+    for a in list(xs.values()) + list(ys.values()):
+        a.free()
+    return out
+
+
 def cpu_gemv_baseline(seconds):
     """Oracle IQ2_XXS GEMV (dequantize + f32 GEMV, one thread), bounded sample:
     alternating [1536 x 2048] and [2048 x 1536] matrices for about `seconds`."""
@@ -457,6 +510,7 @@ def main():
                                   "61 tokens); warm: one layer, one input"}
     out["kv_q8_codec"] = kv_codec_section(ctx, ev, rng)
     out["logits"] = logits_section(ctx, ev, rng)
+    out["mla"] = mla_section(ctx, ev, rng)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_gemv_baseline(args.cpu_seconds)
         out["kv_q8_codec"]["cpu_quantize"] = cpu_kv_codec_baseline(rng)
