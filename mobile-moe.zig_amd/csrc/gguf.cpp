@@ -205,8 +205,10 @@ void describe(const mmhip_gguf& g, const Tensor& t, mmhip_gguf_tensor* out) {
     out->type = t.type;
     out->offset = t.offset;
     uint64_t n = 1;
-    for (uint32_t d = 0; d < t.n_dims; ++d) n *= t.dims[d];
-    out->n_elements = n;
+    bool overflow = false;
+    for (uint32_t d = 0; d < t.n_dims; ++d) overflow |= __builtin_mul_overflow(n, t.dims[d], &n);
+    out->n_elements = overflow ? 0 : n;
+    if (overflow) return;  // no byte count, no data pointer
     const uint64_t bb = block_bytes(t.type), be = block_elems(t.type);
     out->n_bytes = bb ? (n + be - 1) / be * bb : 0;
     // Data pointer only for a type this library reads whose bytes lie inside the file.
@@ -237,6 +239,11 @@ int tensor_matrix(const mmhip_gguf* g, const std::string& name, mmhip_gguf_tenso
     }
     if (t->dims[3] != 1 || t->n_elements == 0) {
         set_error(MMHIP_ERR_INVALID, name + ": not a stack of matrices");
+        return MMHIP_ERR_INVALID;
+    }
+    // The upload reads whole blocks per row: rows must not share a block.
+    if (t->dims[0] % block_elems(t->type) != 0) {
+        set_error(MMHIP_ERR_INVALID, name + ": row length is not a whole number of blocks");
         return MMHIP_ERR_INVALID;
     }
     return MMHIP_OK;

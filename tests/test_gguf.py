@@ -167,3 +167,10 @@ def test_u64_too_large_for_int(tmp_path, lib):
     with _open_bytes(tmp_path, blob) as g:
         with pytest.raises(mm.MmhipError):
             g.meta_int("big")
+
+
+def test_overflowing_dims_have_no_pointer(tmp_path, lib):
+    blob = gw.header(1, 0) + gw.tensor_info("w", [2 ** 33, 2 ** 33, 4], mm.Q8_0, 0)
+    with _open_bytes(tmp_path, blob + b"\0" * 64) as g:
+        t = g.tensor("w")
+        assert t["n_elements"] == 0 and t["n_bytes"] == 0 and not t["data"]

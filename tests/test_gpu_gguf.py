@@ -98,3 +98,13 @@ def test_upload_tensor_by_name(ctx, tmp_path, fmt):
     finally:
         for o in (x, ya, yb, w_file, w_host):
             o.free()
+
+
+def test_upload_rejects_partial_block_rows(ctx, tmp_path):
+    """Rows of 48 Q8_0 values would share a block: refused before any copy."""
+    gw.write(tmp_path / "p.gguf", [], [("w", [48, 2], mm.Q8_0, np.zeros(3 * 34, np.uint8))])
+    with mm.Gguf(tmp_path / "p.gguf") as g:
+        assert g.tensor("w")["data"]
+        with pytest.raises(mm.MmhipError) as e:
+            ctx.upload_gguf(g, "w")
+        assert "whole number of blocks" in str(e.value)
