@@ -309,9 +309,11 @@ def mla_section(ctx, ev, rng, reps=20, n_layers=47, batch=64):
     xs = {n: mm.DeviceArray.from_numpy(ctx, rng.standard_normal(batch * c).astype(np.float32))
           for n, (_, c) in shapes.items()}
     ys = {n: mm.DeviceArray(ctx, batch * r * 4) for n, (r, _) in shapes.items()}
+    ys["qkv_a"] = mm.DeviceArray(ctx, (768 + 576) * 4)
     out = {"workload": f"MLA projections of {n_layers} layers: " +
                        ", ".join(f"{n} [{r}x{c}]" for n, (r, c) in shapes.items()) +
-                       f"; decode = the four GEMVs of one layer, batch = the four products at {batch} tokens"}
+                       f"; decode = the four GEMVs of one layer (fused: q_a and kv_a as one stacked weight), "
+                       f"batch = the four products at {batch} tokens"}
     for name, t in (("q8_0", mm.Q8_0), ("iq2_xxs", mm.IQ2_XXS)):
         raws = {n: mm.make_weight(rng, t, r, c) for n, (r, c) in shapes.items()}
         layers = [{n: ctx.upload(raws[n], t, r, c) for n, (r, c) in shapes.items()} for _ in range(n_layers)]
@@ -329,8 +331,20 @@ def mla_section(ctx, ev, rng, reps=20, n_layers=47, batch=64):
                 ctx.qmm_dev(lw[n], 0, xs[n], ys[n], batch)
             k[0] += 1
 
+        # q_a and kv_a read the same hidden vector: one weight of 768 + 576
+        # stacked rows (the raw rows concatenated), so three launches per layer.
+        qkv = np.concatenate([raws["q_a"], raws["kv_a"]])
+        fused = [ctx.upload(qkv, t, 768 + 576, 2048) for _ in range(n_layers)]
+
+        def decode_fused():
+            lw, i = layers[k[0] % n_layers], k[0] % n_layers
+            ctx.gemv_batched_dev(fused[i], 0, 1, xs["q_a"], 0, ys["qkv_a"], 0)
+            for n in ("q_b", "o_proj"):
+                ctx.gemv_batched_dev(lw[n], 0, 1, xs[n], 0, ys[n], 0)
+            k[0] += 1
+
         res = {}
-        for label, fn in (("decode", decode), ("batch64", prefill)):
+        for label, fn in (("decode", decode), ("decode_fused_qkv_a", decode_fused), ("batch64", prefill)):
             for _ in range(n_layers):
                 fn()
             ctx.synchronize()
@@ -346,6 +360,8 @@ def mla_section(ctx, ev, rng, reps=20, n_layers=47, batch=64):
         for lw in layers:
             for w in lw.values():
                 w.free()
+        for w in fused:
+            w.free()
     for a in list(xs.values()) + list(ys.values()):
         a.free()
     return out

@@ -56,3 +56,19 @@ def test_mla_kv_expansion_f32(ctx, orc, n_pos):
                     for p in range(n_pos)])
     got = ctx.batch_mat_mul(w.view(np.uint8).reshape(-1), mm.F32, kv, NH * NOPE, n_pos, KVL)
     assert mm.max_abs_rel(got, ref) <= TOL_GEMV
+
+
+@pytest.mark.parametrize("fmt", [mm.Q8_0, mm.IQ2_XXS])
+def test_fused_q_a_kv_a(ctx, orc, fmt):
+    """q_a and kv_a read the same hidden vector, so their raw rows stacked into
+    one [1344 x 2048] weight give both projections in one launch: the same
+    bits as the two separate GEMVs, and the oracle's to 1e-3."""
+    rng = np.random.default_rng(500 + fmt)
+    qa, kva = mm.make_weight(rng, fmt, 768, 2048), mm.make_weight(rng, fmt, 576, 2048)
+    qkv = np.concatenate([qa, kva])
+    x = rng.standard_normal(2048).astype(np.float32)
+    fused = ctx.mat_vec_mul(qkv, fmt, x, 768 + 576, 2048)
+    assert np.array_equal(fused[:768].view(np.uint32), ctx.mat_vec_mul(qa, fmt, x, 768, 2048).view(np.uint32))
+    assert np.array_equal(fused[768:].view(np.uint32), ctx.mat_vec_mul(kva, fmt, x, 576, 2048).view(np.uint32))
+    ref = orc.mat_vec_mul_unified(qkv, fmt, x, 768 + 576, 2048)
+    assert mm.max_abs_rel(fused, ref) <= TOL_GEMV
