@@ -265,9 +265,9 @@ int mmhip_gguf_open(const char* path, mmhip_gguf** out) {
         return MMHIP_ERR_INVALID;
     }
     struct stat st;
-    if (fstat(fd, &st) != 0 || st.st_size <= 0) {
+    if (fstat(fd, &st) != 0 || !S_ISREG(st.st_mode) || st.st_size <= 0) {
         close(fd);
-        set_error(MMHIP_ERR_INVALID, std::string("gguf_open: empty or unreadable file ") + path);
+        set_error(MMHIP_ERR_INVALID, std::string("gguf_open: not a non-empty regular file: ") + path);
         return MMHIP_ERR_INVALID;
     }
     void* m = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);

@@ -149,6 +149,12 @@ def test_errors(tmp_path, lib):
         _expect_error(tmp_path, good[:cut], "EndOfStream")
     with pytest.raises(mm.MmhipError):
         mm.Gguf(tmp_path / "missing.gguf")
+    for bad in (tmp_path, tmp_path / "empty.gguf"):
+        if bad != tmp_path:
+            bad.write_bytes(b"")
+        with pytest.raises(mm.MmhipError) as e:
+            mm.Gguf(bad)
+        assert "regular file" in str(e.value) and e.value.code == -2
 
 
 def test_data_outside_file_has_no_pointer(tmp_path, lib):
