@@ -174,6 +174,12 @@ int mmhip_gguf_meta_array(const mmhip_gguf* g, const char* key, uint32_t* elem_t
 /* mmhip_weight_upload of the named tensor (rows = dims[1], cols = dims[0],
  * count = dims[2]). */
 int mmhip_weight_upload_gguf(mmhip_ctx* ctx, const mmhip_gguf* g, const char* name, mmhip_weight** out_w);
+/* One weight whose rows are the named matrices' rows stacked in order (same
+ * type and row length, one matrix each), e.g. attn_q_a then attn_kv_a_mqa,
+ * which read the same hidden vector (src/inference.zig:467-489): one GEMV
+ * launch gives both projections. */
+int mmhip_weight_upload_gguf_rows(mmhip_ctx* ctx, const mmhip_gguf* g, const char* const* names, uint32_t n,
+                                  mmhip_weight** out_w);
 /* mmhip_moe_layer_create from blk.<layer>.ffn_gate_inp / ffn_{gate,up,down}_exps
  * and, when present, ffn_{gate,up,down}_shexp; routed_scaling_factor from
  * <general.architecture>.expert_weights_scale (default 1). */

@@ -405,6 +405,44 @@ int mmhip_weight_upload_gguf(mmhip_ctx* ctx, const mmhip_gguf* g, const char* na
     return mmhip_weight_upload(ctx, t.data, t.type, t.dims[1], t.dims[0], t.dims[2], out_w);
 }
 
+int mmhip_weight_upload_gguf_rows(mmhip_ctx* ctx, const mmhip_gguf* g, const char* const* names, uint32_t n,
+                                  mmhip_weight** out_w) {
+    if (!g || !names || n == 0 || !out_w) {
+        set_error(MMHIP_ERR_INVALID, "weight_upload_gguf_rows: null pointer or no tensors");
+        return MMHIP_ERR_INVALID;
+    }
+    std::vector<mmhip_gguf_tensor> ts(n);
+    uint64_t rows = 0, bytes = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!names[i]) {
+            set_error(MMHIP_ERR_INVALID, "weight_upload_gguf_rows: null tensor name");
+            return MMHIP_ERR_INVALID;
+        }
+        if (int rc = tensor_matrix(g, names[i], &ts[i])) return rc;
+        if (ts[i].dims[2] != 1 || ts[i].type != ts[0].type || ts[i].dims[0] != ts[0].dims[0]) {
+            set_error(MMHIP_ERR_INVALID, std::string("weight_upload_gguf_rows: ") + names[i] +
+                                             " is not one matrix of the first tensor's type and row length");
+            return MMHIP_ERR_INVALID;
+        }
+        rows += ts[i].dims[1];
+        bytes += ts[i].n_bytes;
+    }
+    // Rows of whole blocks are contiguous in GGUF, so the stacked matrix is
+    // the tensors' bytes back to back; it is staged on the device once.
+    void* staging = nullptr;
+    if (int rc = mmhip_malloc(ctx, &staging, bytes)) return rc;
+    int rc = MMHIP_OK;
+    uint64_t off = 0;
+    for (uint32_t i = 0; i < n && rc == MMHIP_OK; ++i) {
+        rc = mmhip_memcpy_h2d(ctx, static_cast<char*>(staging) + off, ts[i].data, ts[i].n_bytes);
+        off += ts[i].n_bytes;
+    }
+    if (rc == MMHIP_OK) rc = mmhip_weight_from_device(ctx, staging, ts[0].type, rows, ts[0].dims[0], 1, out_w);
+    if (rc == MMHIP_OK) rc = mmhip_synchronize(ctx);
+    mmhip_free(ctx, staging);
+    return rc;
+}
+
 int mmhip_moe_layer_create_gguf(mmhip_ctx* ctx, const mmhip_gguf* g, uint32_t layer, mmhip_moe_layer** out_layer) {
     if (!g || !out_layer) {
         set_error(MMHIP_ERR_INVALID, "moe_layer_create_gguf: null pointer");

@@ -136,6 +136,8 @@ _SIGS = {
     "mmhip_gguf_meta_array": (ctypes.c_int, [_c_void_p, ctypes.c_char_p, ctypes.POINTER(_u32), ctypes.POINTER(_u64),
                                              ctypes.POINTER(_c_void_p), ctypes.POINTER(_u64)]),
     "mmhip_weight_upload_gguf": (ctypes.c_int, [_c_void_p, _c_void_p, ctypes.c_char_p, ctypes.POINTER(_c_void_p)]),
+    "mmhip_weight_upload_gguf_rows": (ctypes.c_int, [_c_void_p, _c_void_p, ctypes.POINTER(ctypes.c_char_p), _u32,
+                                                     ctypes.POINTER(_c_void_p)]),
     "mmhip_moe_layer_create_gguf": (ctypes.c_int, [_c_void_p, _c_void_p, _u32, ctypes.POINTER(_c_void_p)]),
     "mmhip_plan_layer": (ctypes.c_int, [_u32, ctypes.POINTER(PlanHParams), ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.POINTER(PerfEntry), ctypes.c_size_t,
@@ -289,6 +291,17 @@ class Context:
               "mmhip_weight_upload_gguf")
         d = t["dims"]
         return Weight(self, h.value, t["type"], d[1], d[0], d[2])
+
+    def upload_gguf_rows(self, g: "Gguf", names) -> Weight:
+        """One weight of the named matrices' rows stacked in order (e.g. q_a then kv_a)."""
+        ts = [g.tensor(n) for n in names]
+        if any(t is None for t in ts):
+            raise KeyError([n for n, t in zip(names, ts) if t is None])
+        arr = (ctypes.c_char_p * len(names))(*[n.encode() for n in names])
+        h = _c_void_p()
+        check(self.lib.mmhip_weight_upload_gguf_rows(self.handle, g.handle, arr, len(names), ctypes.byref(h)),
+              "mmhip_weight_upload_gguf_rows")
+        return Weight(self, h.value, ts[0]["type"], sum(t["dims"][1] for t in ts), ts[0]["dims"][0], 1)
 
     def weight_from_device(self, raw: DeviceArray, ggml_type: int, rows: int, cols: int, count: int = 1) -> Weight:
         h = _c_void_p()

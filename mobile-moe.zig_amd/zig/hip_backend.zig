@@ -128,6 +128,7 @@ extern fn mmhip_gguf_meta_float(g: *const GgufHandle, key: [*:0]const u8, out: *
 extern fn mmhip_gguf_meta_string(g: *const GgufHandle, key: [*:0]const u8, str: *?[*]const u8, len: *u64) c_int;
 extern fn mmhip_gguf_meta_array(g: *const GgufHandle, key: [*:0]const u8, elem_type: *u32, len: *u64, data: *?*const anyopaque, n_bytes: *u64) c_int;
 extern fn mmhip_weight_upload_gguf(ctx: *Ctx, g: *const GgufHandle, name: [*:0]const u8, out_w: *?*Weight) c_int;
+extern fn mmhip_weight_upload_gguf_rows(ctx: *Ctx, g: *const GgufHandle, names: [*]const [*:0]const u8, n: u32, out_w: *?*Weight) c_int;
 extern fn mmhip_moe_layer_create_gguf(ctx: *Ctx, g: *const GgufHandle, layer: u32, out_layer: *?*MoeLayerHandle) c_int;
 extern fn mmhip_weight_upload(ctx: *Ctx, raw_host: ?*const anyopaque, type_: u32, rows: u64, cols: u64, count: u64, out_w: *?*Weight) c_int;
 extern fn mmhip_weight_from_device(ctx: *Ctx, raw_dev: ?*const anyopaque, type_: u32, rows: u64, cols: u64, count: u64, out_w: *?*Weight) c_int;
@@ -396,6 +397,14 @@ pub const GgufFile = struct {
         if (mmhip_gguf_meta_array(self.handle, key, &et, &n, &d, &nb) != 0) return null;
         const bytes: []const u8 = if (nb == 0) "" else @as([*]const u8, @ptrCast(d.?))[0..@intCast(nb)];
         return .{ .elem_type = et, .len = n, .data = bytes };
+    }
+
+    /// One weight of several matrices' rows stacked in order (same type and
+    /// row length), e.g. attn_q_a then attn_kv_a_mqa: one GEMV for both.
+    pub fn uploadRows(self: *const GgufFile, backend: *HipBackend, names: []const [*:0]const u8) !*Weight {
+        var w: ?*Weight = null;
+        try check(mmhip_weight_upload_gguf_rows(backend.ctx, self.handle, names.ptr, @intCast(names.len), &w));
+        return w.?;
     }
 
     /// One-time device upload of a tensor ([cols, rows, count] in ggml order).

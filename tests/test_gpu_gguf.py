@@ -108,3 +108,35 @@ def test_upload_rejects_partial_block_rows(ctx, tmp_path):
         with pytest.raises(mm.MmhipError) as e:
             ctx.upload_gguf(g, "w")
         assert "whole number of blocks" in str(e.value)
+
+
+@pytest.mark.parametrize("fmt", [mm.Q8_0, mm.IQ2_XXS])
+def test_upload_stacked_rows(ctx, tmp_path, fmt):
+    """attn_q_a [768 x 2048] and attn_kv_a_mqa [576 x 2048] stacked into one
+    weight from the file: the same bits as each uploaded and run alone."""
+    rng = np.random.default_rng(120 + fmt)
+    qa, kva = mm.make_weight(rng, fmt, 768, 2048), mm.make_weight(rng, fmt, 576, 2048)
+    names = ["blk.1.attn_q_a.weight", "blk.1.attn_kv_a_mqa.weight"]
+    gw.write(tmp_path / "a.gguf", [], [(names[0], [2048, 768], fmt, qa), ("blk.1.attn_norm.weight", [7], mm.F32,
+                                                                          np.ones(7, np.float32)),
+                                       (names[1], [2048, 576], fmt, kva)])
+    print(f"gguf stacked rows fmt={fmt}", flush=True)
+    with mm.Gguf(tmp_path / "a.gguf") as g:
+        w = ctx.upload_gguf_rows(g, names)
+        with pytest.raises(mm.MmhipError):
+            ctx.upload_gguf_rows(g, [names[0], "blk.1.attn_norm.weight"])  # another type and row length
+    parts = [ctx.upload(qa, fmt, 768, 2048), ctx.upload(kva, fmt, 576, 2048)]
+    x = mm.DeviceArray.from_numpy(ctx, rng.standard_normal(2048).astype(np.float32))
+    y, y0, y1 = mm.DeviceArray(ctx, 1344 * 4), mm.DeviceArray(ctx, 768 * 4), mm.DeviceArray(ctx, 576 * 4)
+    try:
+        assert w.rows == 1344 and w.cols == 2048
+        ctx.gemv_batched_dev(w, 0, 1, x, 0, y, 0)
+        ctx.gemv_batched_dev(parts[0], 0, 1, x, 0, y0, 0)
+        ctx.gemv_batched_dev(parts[1], 0, 1, x, 0, y1, 0)
+        ctx.synchronize()
+        a = y.to_numpy(np.float32, 1344)
+        b = np.concatenate([y0.to_numpy(np.float32, 768), y1.to_numpy(np.float32, 576)])
+        assert np.isfinite(a).all() and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    finally:
+        for o in [x, y, y0, y1, w] + parts:
+            o.free()
