@@ -181,8 +181,9 @@ int mmhip_weight_upload_gguf(mmhip_ctx* ctx, const mmhip_gguf* g, const char* na
 int mmhip_weight_upload_gguf_rows(mmhip_ctx* ctx, const mmhip_gguf* g, const char* const* names, uint32_t n,
                                   mmhip_weight** out_w);
 /* mmhip_moe_layer_create from blk.<layer>.ffn_gate_inp / ffn_{gate,up,down}_exps
- * and, when present, ffn_{gate,up,down}_shexp; routed_scaling_factor from
- * <general.architecture>.expert_weights_scale (default 1). */
+ * and, when present, ffn_{gate,up,down}_shexp (the shared width is their
+ * row count); routed_scaling_factor from deepseek2.expert_weights_scale
+ * (default 1), the key HyperParams.fromGguf reads (model.zig:107). */
 int mmhip_moe_layer_create_gguf(mmhip_ctx* ctx, const mmhip_gguf* g, uint32_t layer,
                                 mmhip_moe_layer** out_layer);
 
@@ -208,10 +209,13 @@ int mmhip_dequantize(mmhip_ctx* ctx, float* out_host, const void* data_host,
 /* quantizeQ8_0 (dequant.zig:98-130): n floats -> ceil(n / 32) raw Q8_0
  * blocks of 34 bytes (per block: d = max|x| / 127 stored as f16, q = x / d
  * rounded half away from zero, clamped to +-127; the last block padded with
- * zeros). Bit-exact with the CPU path; where a block scale falls in the f16
- * subnormal range (max|x| < 127 * 2^-14), for which the reference's f32ToF16
- * has no defined result (its shift overflows the 10-bit field), the scale is
- * the subnormal value truncated toward zero. A NaN value quantises to 0. */
+ * zeros). Bit-exact with the CPU path except on the f16 subnormal range of
+ * the block scale, d in [2^-25, 2^-14), where the reference's f32ToF16
+ * (dequant.zig:76-77) shifts the significand by 1 - exp16: for d in
+ * [2^-21, 2^-14) its @intCast traps, and for d in [2^-25, 2^-21) it returns a
+ * corrupted code (e.g. d = 2^-22 -> 0x8000, d = 1.5 * 2^-23 -> 0x6000). Here
+ * the scale on that whole range is the subnormal value truncated toward
+ * zero (d = 2^-22 -> 0x0004). A NaN value quantises to 0. */
 int mmhip_quantize_q8_0(mmhip_ctx* ctx, void* blocks_host, const float* x_host,
                         uint64_t n_elements);
 /* sampleGreedy (inference.zig:376-386) over n logits (computeLogits'

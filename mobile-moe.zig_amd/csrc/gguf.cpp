@@ -437,8 +437,9 @@ int mmhip_weight_upload_gguf_rows(mmhip_ctx* ctx, const mmhip_gguf* g, const cha
         rc = mmhip_memcpy_h2d(ctx, static_cast<char*>(staging) + off, ts[i].data, ts[i].n_bytes);
         off += ts[i].n_bytes;
     }
+    // weight_from_device synchronises after its repack, so the staging copy
+    // is free to release once it returns; on failure *out_w stays null.
     if (rc == MMHIP_OK) rc = mmhip_weight_from_device(ctx, staging, ts[0].type, rows, ts[0].dims[0], 1, out_w);
-    if (rc == MMHIP_OK) rc = mmhip_synchronize(ctx);
     mmhip_free(ctx, staging);
     return rc;
 }
@@ -476,14 +477,12 @@ int mmhip_moe_layer_create_gguf(mmhip_ctx* ctx, const mmhip_gguf* g, uint32_t la
     w.expert_down_host = down.data;
     w.shared_type = gate.type;
     w.shared_intermediate = (uint32_t)inter;
-    // HyperParams.fromGguf: routed_scaling_factor = <arch>.expert_weights_scale, default 1.
+    // HyperParams.fromGguf (model.zig:107): routed_scaling_factor =
+    // deepseek2.expert_weights_scale, default 1, whatever general.architecture says.
     w.routed_scaling_factor = 1.0f;
-    const char* arch = nullptr;
-    uint64_t arch_len = 0;
-    if (mmhip_gguf_meta_string(g, "general.architecture", &arch, &arch_len) == MMHIP_OK) {
+    {
         double s;
-        if (mmhip_gguf_meta_float(g, (std::string(arch, arch_len) + ".expert_weights_scale").c_str(), &s) == MMHIP_OK)
-            w.routed_scaling_factor = (float)s;
+        if (mmhip_gguf_meta_float(g, "deepseek2.expert_weights_scale", &s) == MMHIP_OK) w.routed_scaling_factor = (float)s;
     }
     mmhip_gguf_tensor sg;
     if (mmhip_gguf_find_tensor(g, (p + "ffn_gate_shexp.weight").c_str(), &sg) == MMHIP_OK) {

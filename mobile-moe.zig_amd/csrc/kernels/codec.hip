@@ -208,10 +208,11 @@ __global__ __launch_bounds__(256) void quantize_wide_kernel(const float* __restr
 
 // f32ToF16 (dequant.zig:50-95) as the quantiser stores a block scale: round
 // to nearest even on the normal range, 0 for f32 subnormals and below 2^-25,
-// Inf / NaN kept. On the f16 subnormal range the reference shifts the
-// significand by 1 - e16, which overflows the 10-bit field (a trap in safe
-// builds, so it defines no result); this takes the branch's evident intent,
-// a shift by 14 - e16: the subnormal value truncated toward zero.
+// Inf / NaN kept. On the f16 subnormal range, [2^-25, 2^-14), the reference
+// shifts the significand by 1 - e16, which spills out of the 10-bit field: a
+// trap in safe builds for [2^-21, 2^-14), a corrupted code for [2^-25, 2^-21)
+// (2^-22 -> 0x8000). This takes the branch's evident intent on the whole
+// range, a shift by 14 - e16: the subnormal value truncated toward zero.
 __device__ __forceinline__ uint32_t f32_to_f16_scale(float v) {
     const uint32_t bits = __float_as_uint(v);
     const uint32_t er = (bits >> 23) & 0xFFu, mant = bits & 0x7FFFFFu;

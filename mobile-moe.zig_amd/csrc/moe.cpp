@@ -313,8 +313,13 @@ int call_params(const mmhip_moe_layer* L, uint32_t T, const mmhip_route_params* 
         set_error(MMHIP_ERR_INVALID, "moe: n_tokens must be in [1, " + std::to_string(kMaxTok) + "]");
         return MMHIP_ERR_INVALID;
     }
-    int lv = rp ? rp->throttle_level : 0;
-    if (lv < 0 || lv > 3) lv = 0;
+    const int lv = rp ? rp->throttle_level : 0;
+    if (lv < 0 || lv > 3) {
+        // ThrottleLevel has four values (thermal.zig:17-22); anything else is a
+        // caller error, not a reason to run unthrottled.
+        set_error(MMHIP_ERR_INVALID, "moe: throttle_level must be in [0, 3], got " + std::to_string(lv));
+        return MMHIP_ERR_INVALID;
+    }
     const uint32_t limit = (rp && rp->active_expert_limit) ? rp->active_expert_limit : level_limit(lv);
     uint32_t kk = limit < 4 ? limit : 4;
     if (kk > L->n_experts) kk = L->n_experts;

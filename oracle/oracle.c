@@ -50,12 +50,19 @@ float orc_f16_to_f32(uint16_t h) {
 }
 
 /* f32ToF16, dequant.zig:50-95. Normal results round to nearest-even (82-90);
- * f32 zero/subnormal inputs and results below 2^-24 flush to zero (59-61,
- * 72-74). Subnormal-result branch (76-77): the reference shifts the 24-bit
- * significand right by (1 - exp16) instead of (14 - exp16), so the "mantissa"
- * overflows 10 bits and the final @intCast to u16 traps in safe builds. The
- * restatement reports that case through *defect (and returns the low 16
- * bits); nothing on the hot path converts to f16. */
+ * f32 zero/subnormal inputs and values below 2^-25 (exp16 < -10) flush to
+ * zero (59-61, 72-74). Subnormal-result branch (76-77), exp16 in [-10, 0],
+ * i.e. v in [2^-25, 2^-14): the reference shifts the 24-bit significand
+ * right by (1 - exp16) instead of (14 - exp16), so m keeps 23 + exp16 bits
+ * and spills out of the 10-bit field:
+ *   v in [2^-21, 2^-14) (exp16 >= -6): m >= 2^16, the final @intCast to u16
+ *     traps in safe builds; *defect = 1 and the low 16 bits are returned;
+ *   v in [2^-25, 2^-21) (exp16 <= -7): m < 2^16, so the reference returns a
+ *     defined but wrong code (m's high bits land in the exponent and sign
+ *     fields: 2^-22 -> 0x8000 = -0.0, 1.5 * 2^-23 -> 0x6000 = 512.0);
+ *     *defect = 2 and that code is returned.
+ * Nothing on the hot path converts to f16; quantizeQ8_0's scale uses
+ * f32_to_f16_scale below. */
 uint16_t orc_f32_to_f16(float v, int* defect) {
     uint32_t bits = f32_to_bits(v);
     uint32_t sign = (bits >> 31) & 1u;
@@ -79,7 +86,7 @@ uint16_t orc_f32_to_f16(float v, int* defect) {
             } else {
                 e = 0;
                 m = (mant | 0x800000u) >> (uint32_t)(1 - e16);
-                if (defect) *defect = 1;
+                if (defect) *defect = m > 0xFFFFu ? 1 : 2;
             }
         } else {
             e = (uint32_t)e16;
@@ -95,10 +102,11 @@ uint16_t orc_f32_to_f16(float v, int* defect) {
 }
 
 /* f32ToF16 as quantizeQ8_0 / KVCache.put store a block scale. Same as
- * orc_f32_to_f16 except where the reference's subnormal branch overflows
- * (above; a trap in safe builds, so the reference defines no result there):
- * this uses the branch's evident intent, the significand shifted by
- * 14 - e16, i.e. the subnormal result truncated toward zero. */
+ * orc_f32_to_f16 except on the whole subnormal-result range [2^-25, 2^-14)
+ * (above): where the reference traps ([2^-21, 2^-14)) and where it returns a
+ * corrupted code ([2^-25, 2^-21)), this uses the branch's evident intent,
+ * the significand shifted by 14 - e16, i.e. the subnormal value truncated
+ * toward zero. A deliberate fix, not the reference's bits. */
 static uint16_t f32_to_f16_scale(float v) {
     int defect = 0;
     uint16_t h = orc_f32_to_f16(v, &defect);

@@ -18,8 +18,9 @@
  *                           65,536-code comparison with IEEE binary16->32.
  *   orc_f32_to_f16          reference KATs (1.0, 2.0, 0.5, 1/127) + numpy RNE
  *                           on the normal range; the subnormal branch is a
- *                           reference defect (see the function) and is only
- *                           checked to report it.
+ *                           reference defect (see the function): *defect = 1
+ *                           where the reference traps, 2 where it returns a
+ *                           corrupted code, pinned by hand-derived codes.
  *   orc_dequantize_q8_0     closed form d*q (exact in f32) on all 65,536 d codes.
  *   orc_sample_greedy       numpy argmax (first occurrence) on NaN-free data,
  *                           hand-derived cases: ties, -0 vs +0, NaN at 0 and

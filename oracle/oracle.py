@@ -97,9 +97,12 @@ def f16_to_f32(h: int) -> float:
 
 
 def f32_to_f16(v: float):
+    """f32ToF16 (dequant.zig:50-95): (code, defect) with defect 0 (a correct
+    code), 1 (the reference traps; low 16 bits returned) or 2 (the reference
+    returns this corrupted code)."""
     d = ctypes.c_int(0)
     r = lib().orc_f32_to_f16(v, ctypes.byref(d))
-    return r, bool(d.value)
+    return r, d.value
 
 
 def sample_greedy(logits: np.ndarray) -> int:

@@ -260,6 +260,12 @@ def test_invalid_calls(ctx, orc):
             gpu.ffn(np.zeros((0, SMALL["H"]), np.float32))
         with pytest.raises(mm.MmhipError):
             gpu.ffn(np.zeros((257, SMALL["H"]), np.float32))
+        # ThrottleLevel has four values (thermal.zig:10-15): others are errors,
+        # not an unthrottled call.
+        h = rng.standard_normal((1, SMALL["H"])).astype(np.float32)
+        for bad in (-1, 4, 7):
+            with pytest.raises(mm.MmhipError, match="throttle_level"):
+                gpu.ffn(h, level=bad)
     finally:
         gpu.free()
 

@@ -95,3 +95,30 @@ def test_subnormal_scale_truncates(orc):
     assert d16[0] == int(np.floor(float(d) / 2.0 ** -24))
     assert qs[0, 5] == 127 and qs[0, 6] == int(_nearest_away(float(np.float32(np.float32(-3e-5) / d))))
 
+
+
+def test_subnormal_scale_ranges_against_reference_codes(orc):
+    """The reference's subnormal branch (dequant.zig:76-77) computes
+    m = (mant | 2^23) >> (1 - exp16) and returns (sign << 15) | m via @intCast.
+    Worked by hand from those lines:
+      d = 2^-20   (exp16 = -5): m = 2^23 >> 6 = 2^17 > 0xFFFF -> @intCast traps;
+      d = 2^-22   (exp16 = -7): m = 2^23 >> 8 = 0x8000 -> code 0x8000 (-0.0);
+      d = 1.5 * 2^-23 (exp16 = -8): m = 0xC00000 >> 9 = 0x6000 -> 512.0;
+      d = 2^-25   (exp16 = -10): m = 2^23 >> 11 = 0x1000 -> 2^-11.
+    quantizeQ8_0 here stores the subnormal scale truncated toward zero
+    instead (d / 2^-24 rounded down), a deliberate fix: next to each
+    reference code, the stored one."""
+    cases = [(2.0 ** -20, None, 0x0010), (2.0 ** -22, 0x8000, 0x0004), (1.5 * 2.0 ** -23, 0x6000, 0x0003),
+             (2.0 ** -25, 0x1000, 0x0000)]
+    for d, ref_code, stored in cases:
+        h, defect = orc.f32_to_f16(d)
+        if ref_code is None:
+            assert defect == 1
+        else:
+            assert defect == 2 and h == ref_code, (d, hex(h))
+        # a block whose max |x| is 127 d: d = max / 127 is exact in f32
+        x = np.zeros(32, dtype=np.float32)
+        x[3] = np.float32(127.0 * d)
+        d16, qs = _blocks(orc.quantize_q8_0(x))
+        assert d16[0] == stored == int(np.floor(d / 2.0 ** -24)), (d, hex(int(d16[0])))
+        assert qs[0, 3] == 127
