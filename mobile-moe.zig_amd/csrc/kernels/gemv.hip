@@ -9,7 +9,8 @@
 // (gemv_iq2.hip); launch_gemv_q forwards them there.
 //
 // f32 / f16 weights (the router, matVecMulUnified's f32 branch): one
-// workgroup per output row.
+// workgroup per output row, summing in the reference's order
+// (gemv_strict_kernel).
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "route_ops.hpp"
@@ -253,83 +254,107 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     }
 }
 
-// f32 / f16 weights: one 256-thread workgroup per output row and NT
-// vectors (NT > 1 only when all vectors share one matrix, as a batch of
-// tokens shares the router): the row's columns are loaded once and used for
-// every vector. Each pass covers 2048 columns (8 per thread) with all of a
-// thread's loads in flight together; out-of-range columns, and vectors past
-// n_mats, read as zero through the buffer resources. A vector's sum runs in
-// the same order whatever NT is, so a token's scores do not depend on the
-// batch it came in.
+// f32 / f16 weights (the router, matVecMulUnified's f32 branch): the
+// reference's summation order, bit for bit. math.matVecMul (math.zig:79-99)
+// keeps four accumulators, lane l summing the products of columns
+// l, l + 4, l + 8, ... in column order (each product rounded, then added:
+// no fused multiply-add), adds them as ((a0 + a1) + a2) + a3 (@reduce over a
+// 4-vector) and then the remaining cols % 4 products one by one. f16 weights
+// are widened exactly first, as dequantize does (dequant.zig:632-659).
+//
+// A rounded sequential sum has no parallel form, so each lane's chain runs
+// in one thread. A 256-thread workgroup owns one row and NV vectors (NV > 1
+// when the vectors share the matrix, as a batch of tokens shares the
+// router): per chunk of kStrictChunk columns every thread forms products of
+// its column quads (one load of the row's quad serves all NV vectors) and
+// stores them de-interleaved, P[4v + l][i] for column 4i + l, so that chain
+// (v, l) then reads four consecutive terms per LDS access and only adds.
+// Products of vectors past n_vecs and columns past cols4 read as zero
+// through the buffer resources and are never summed.
 constexpr int kFloatThreads = 256;
-// Four f32 at element e (4-aligned when vec).
-__device__ __forceinline__ void load4(BufRsrc r, uint32_t e, bool vec, float* out) {
-    if (vec) {
-        const uint4 v = buf_load_b128(r, e * 4, 0);
-        out[0] = __uint_as_float(v.x);
-        out[1] = __uint_as_float(v.y);
-        out[2] = __uint_as_float(v.z);
-        out[3] = __uint_as_float(v.w);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(buf_load_b32(r, (e + i) * 4, 0));
-    }
-}
-template <typename WT, int NT>
-__global__ __launch_bounds__(kFloatThreads) void gemv_float_kernel(const WT* __restrict__ w, uint64_t mat_stride,
-                                                                   const float* __restrict__ x, uint64_t x_stride,
-                                                                   float* __restrict__ y, uint64_t y_stride,
-                                                                   uint32_t n_mats, uint32_t rows, uint32_t cols) {
-    __shared__ float part[NT][kFloatThreads / 64];
-    const uint32_t m0 = blockIdx.y * NT, r = blockIdx.x;
-    const bool vec = cols % 4 == 0;  // 16-byte loads; otherwise one load per column (per-column bounds)
-    const BufRsrc wr = make_rsrc(w + m0 * mat_stride + (uint64_t)r * cols, cols * (uint32_t)sizeof(WT));
-    float acc[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[j] = 0.0f;
-    for (uint32_t c0 = 0; c0 < cols; c0 += kFloatThreads * 8) {
-        const uint32_t c = c0 + threadIdx.x * 4;
-        float wv[8];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t cc = c + h * kFloatThreads * 4;
+
+template <typename WT, int NV>
+__global__ __launch_bounds__(kFloatThreads) void gemv_strict_kernel(const WT* __restrict__ w, uint64_t mat_stride,
+                                                                    const float* __restrict__ x, uint64_t x_stride,
+                                                                    float* __restrict__ y, uint64_t y_stride,
+                                                                    uint32_t n_vecs, uint32_t rows, uint32_t cols) {
+#pragma clang fp contract(off)
+    // Columns per product chunk (multiple of 16); a chain's row is padded by
+    // four floats so the 16 chains of a lane group read disjoint banks.
+    constexpr uint32_t kStrictChunk = NV == 1 ? 2048 : 512;
+    constexpr uint32_t kPRow = kStrictChunk / 4 + 4;
+    __shared__ __align__(16) float P[NV * 4][kPRow];
+    const uint32_t r = blockIdx.x, v0 = blockIdx.y * NV;
+    const uint32_t cols4 = cols & ~3u;
+    // Vector v0 + j's matrix: one shared matrix (mat_stride 0) or one each.
+    const WT* wrow = w + (uint64_t)(NV == 1 ? v0 : 0) * mat_stride + (uint64_t)r * cols;
+    const BufRsrc wr = make_rsrc(wrow, cols4 * (uint32_t)sizeof(WT));
+    const uint32_t tid = threadIdx.x;
+    // Chain thread: lanes 4v + l of wave 0 (NV <= 16).
+    const uint32_t cv = tid >> 2, cl = tid & 3;
+    const bool chain = tid < 4u * NV;
+    float acc = 0.0f;
+    for (uint32_t c0 = 0; c0 < cols4; c0 += kStrictChunk) {
+        const uint32_t cn = min(kStrictChunk, cols4 - c0);
+        // Product phase: column quad q = c0 / 4 + i, i = tid + 256 k.
+        for (uint32_t i = tid; i < cn / 4; i += kFloatThreads) {
+            const uint32_t col = c0 + 4 * i;
+            float wv[4];
             if constexpr (sizeof(WT) == 2) {
-                if (vec) {
-                    const uint2 hv = buf_load_b64(wr, cc * 2, 0);
-                    wv[4 * h + 0] = f16_bits_to_f32(hv.x & 0xFFFFu);
-                    wv[4 * h + 1] = f16_bits_to_f32(hv.x >> 16);
-                    wv[4 * h + 2] = f16_bits_to_f32(hv.y & 0xFFFFu);
-                    wv[4 * h + 3] = f16_bits_to_f32(hv.y >> 16);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) wv[4 * h + e] = f16_bits_to_f32(buf_load_b16(wr, (cc + e) * 2, 0));
-                }
+                const uint2 hv = buf_load_b64(wr, col * 2, 0);
+                wv[0] = f16_bits_to_f32(hv.x & 0xFFFFu);
+                wv[1] = f16_bits_to_f32(hv.x >> 16);
+                wv[2] = f16_bits_to_f32(hv.y & 0xFFFFu);
+                wv[3] = f16_bits_to_f32(hv.y >> 16);
             } else {
-                load4(wr, cc, vec, wv + 4 * h);
+                const uint4 q = buf_load_b128(wr, col * 4, 0);
+                wv[0] = __uint_as_float(q.x);
+                wv[1] = __uint_as_float(q.y);
+                wv[2] = __uint_as_float(q.z);
+                wv[3] = __uint_as_float(q.w);
+            }
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const uint32_t m = v0 + j;
+                const BufRsrc xr = make_rsrc(x + (uint64_t)(m < n_vecs ? m : 0) * x_stride, m < n_vecs ? cols4 * 4 : 0);
+                const uint4 q = buf_load_b128(xr, col * 4, 0);
+                P[4 * j + 0][i] = wv[0] * __uint_as_float(q.x);
+                P[4 * j + 1][i] = wv[1] * __uint_as_float(q.y);
+                P[4 * j + 2][i] = wv[2] * __uint_as_float(q.z);
+                P[4 * j + 3][i] = wv[3] * __uint_as_float(q.w);
             }
         }
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const uint32_t m = m0 + j;
-            const BufRsrc xr = make_rsrc(x + (uint64_t)(m < n_mats ? m : 0) * x_stride, m < n_mats ? cols * 4 : 0);
-            float xv[8];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) load4(xr, c + h * kFloatThreads * 4, vec, xv + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[j] = fmaf(wv[e], xv[e], acc[j]);
+        __syncthreads();
+        if (chain) {
+            const float4* pp = reinterpret_cast<const float4*>(&P[tid][0]);
+            for (uint32_t i = 0; i < cn / 16; ++i) {
+                const float4 t = pp[i];
+                acc = acc + t.x;
+                acc = acc + t.y;
+                acc = acc + t.z;
+                acc = acc + t.w;
+            }
+            // cn is a multiple of 4 but not always of 16: the last quad-steps.
+            for (uint32_t i = (cn / 16) * 4; i < cn / 4; ++i) acc = acc + P[tid][i];
         }
+        __syncthreads();
     }
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const float v = wave_sum(acc[j]);
-        if ((threadIdx.x & 63) == 0) part[j][threadIdx.x >> 6] = v;
-    }
-    __syncthreads();
-    if (threadIdx.x < NT && m0 + threadIdx.x < n_mats) {
-        float t = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kFloatThreads / 64; ++i) t += part[threadIdx.x][i];
-        y[(m0 + threadIdx.x) * y_stride + r] = t;
+    // ((a0 + a1) + a2) + a3 in lane l = 0 of each chain, then the tail.
+    const float a1 = __shfl_down(acc, 1, kWave), a2 = __shfl_down(acc, 2, kWave), a3 = __shfl_down(acc, 3, kWave);
+    if (chain && cl == 0 && v0 + cv < n_vecs) {
+        const uint32_t m = v0 + cv;
+        float sum = ((acc + a1) + a2) + a3;
+        const WT* wm = w + (uint64_t)(NV == 1 ? m : 0) * mat_stride + (uint64_t)r * cols;
+        const float* xm = x + (uint64_t)m * x_stride;
+        for (uint32_t j = cols4; j < cols; ++j) {
+            float wj;
+            if constexpr (sizeof(WT) == 2)
+                wj = f16_bits_to_f32(wm[j]);
+            else
+                wj = wm[j];
+            sum = sum + wj * xm[j];
+        }
+        y[(uint64_t)m * y_stride + r] = sum;
     }
 }
 
@@ -424,20 +449,20 @@ hipError_t launch_gemv_float(const void* w, uint32_t type, uint64_t mat_stride, 
         // One matrix, several vectors: 16 vectors per workgroup.
         const dim3 grid(rows, (n_mats + 15) / 16);
         if (type == 0)
-            gemv_float_kernel<float, 16><<<grid, kFloatThreads, 0, s>>>((const float*)w, 0, x, x_stride, y, y_stride,
-                                                                        n_mats, rows, cols);
+            gemv_strict_kernel<float, 16><<<grid, kFloatThreads, 0, s>>>((const float*)w, 0, x, x_stride, y, y_stride,
+                                                                         n_mats, rows, cols);
         else
-            gemv_float_kernel<uint16_t, 16><<<grid, kFloatThreads, 0, s>>>((const uint16_t*)w, 0, x, x_stride, y,
-                                                                           y_stride, n_mats, rows, cols);
+            gemv_strict_kernel<uint16_t, 16><<<grid, kFloatThreads, 0, s>>>((const uint16_t*)w, 0, x, x_stride, y,
+                                                                            y_stride, n_mats, rows, cols);
         return hipGetLastError();
     }
     const dim3 grid(rows, n_mats);
     if (type == 0)
-        gemv_float_kernel<float, 1><<<grid, kFloatThreads, 0, s>>>((const float*)w, mat_stride, x, x_stride, y,
-                                                                   y_stride, n_mats, rows, cols);
+        gemv_strict_kernel<float, 1><<<grid, kFloatThreads, 0, s>>>((const float*)w, mat_stride, x, x_stride, y,
+                                                                    y_stride, n_mats, rows, cols);
     else
-        gemv_float_kernel<uint16_t, 1><<<grid, kFloatThreads, 0, s>>>((const uint16_t*)w, mat_stride, x, x_stride, y,
-                                                                      y_stride, n_mats, rows, cols);
+        gemv_strict_kernel<uint16_t, 1><<<grid, kFloatThreads, 0, s>>>((const uint16_t*)w, mat_stride, x, x_stride, y,
+                                                                       y_stride, n_mats, rows, cols);
     return hipGetLastError();
 }
 

@@ -33,13 +33,36 @@ def test_gemv_config_shapes(ctx, orc, t, rows, cols):
     assert err <= TOL_GEMV
 
 
+def _bits_equal(got, ref):
+    """Bit-exact comparison of float results (NaN-free data)."""
+    got = np.ascontiguousarray(got, dtype=np.float32)
+    ref = np.ascontiguousarray(ref, dtype=np.float32)
+    assert got.shape == ref.shape
+    bad = np.flatnonzero(got.view(np.uint32) != ref.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} results differ, first at {bad[0]}: {got.flat[bad[0]]!r} vs {ref.flat[bad[0]]!r}"
+
+
 @pytest.mark.parametrize("t", [mm.F32, mm.F16])
 def test_gemv_float_router_shape(ctx, orc, t):
+    """f32 / f16 weights sum in math.matVecMul's order (math.zig:79-99: four
+    lane accumulators, unfused products, ((a0 + a1) + a2) + a3, then the
+    tail), so the router's scores are the CPU path's bits."""
     rng = np.random.default_rng(40 + t)
     raw = _weights(rng, t, 64, 2048)
     x = rng.standard_normal(2048).astype(np.float32)
     ref = orc.mat_vec_mul_unified(raw, t, x, 64, 2048)
-    assert mm.max_abs_rel(ctx.mat_vec_mul(raw, t, x, 64, 2048), ref) <= 1e-5
+    _bits_equal(ctx.mat_vec_mul(raw, t, x, 64, 2048), ref)
+
+
+@pytest.mark.parametrize("t", [mm.F32, mm.F16])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (7, 33), (2, 2050), (5, 4099), (64, 6144), (2560, 512)])
+def test_gemv_float_bit_exact_shapes(ctx, orc, t, rows, cols):
+    """Tails of 1-3 columns, several product chunks, MLA's k_b / v_b expansion
+    shape [2560 x 512] (inference.zig:539-544): bit-exact."""
+    rng = np.random.default_rng(rows * 31 + cols + t)
+    raw = _weights(rng, t, rows, cols)
+    x = (rng.standard_normal(cols) * 3.0).astype(np.float32)
+    _bits_equal(ctx.mat_vec_mul(raw, t, x, rows, cols), orc.mat_vec_mul_unified(raw, t, x, rows, cols))
 
 
 @pytest.mark.parametrize("t,rows,cols", [
@@ -156,16 +179,17 @@ def test_qmm_batch64_config(ctx, orc, t, rows, cols):
 @pytest.mark.parametrize("batch,rows,cols", [(5, 80, 320), (16, 64, 2048), (37, 200, 1024), (64, 64, 2048),
                                              (9, 48, 330)])
 def test_float_weights_batched(ctx, orc, t, batch, rows, cols):
-    """f32 / f16 weights times a batch (the router of a prefill call): batches
-    above 4 with columns a multiple of 4 run as 16 x 16 f32 MFMA tiles; rows
-    and batches that are not multiples of 16 leave partial tiles; 330 columns
-    take the one-row-per-workgroup kernel. f32 accumulation: TOL_GEMV."""
+    """f32 / f16 weights times a batch (the router of a prefill call,
+    batchMatMulUnified's f32 branch: one math.matVecMul per row,
+    inference.zig:1256-1262): 16 vectors per workgroup share each row's
+    loads, and every vector's sum keeps the single-vector order, so the
+    results are the CPU path's bits for any batch."""
     rng = np.random.default_rng(batch * 7 + rows + t)
     raw = _weights(rng, t, rows, cols)
     xin = rng.standard_normal((batch, cols)).astype(np.float32)
     ref = orc.batch_mat_mul_unified(raw, t, xin, rows, batch, cols)
     got = ctx.batch_mat_mul(raw, t, xin, rows, batch, cols)
-    assert mm.max_abs_rel(got, ref) <= TOL_GEMV
+    _bits_equal(got, ref)
 
 
 @pytest.mark.parametrize("batch", [1, 2, 7, 33, 100])
