@@ -266,6 +266,21 @@ int mmhip_qmm_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat,
                   const float* x_dev, float* y_dev, uint64_t batch,
                   int out_layout);
 
+/* mmhip_qmm_dev without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts
+ * that forbid hipMalloc). No counterpart in the reference. Same kernels and
+ * results as mmhip_qmm_dev; the quantised activations go to a fixed scratch
+ * of MMHIP_NOALLOC_SCRATCH_BYTES per device, held until the process ends, so
+ * quantised weights need batch x cols256 x 2.125 <= MMHIP_NOALLOC_SCRATCH_BYTES
+ * (cols256 = cols rounded up to 256: e.g. 256 rows of 8192 columns), else
+ * MMHIP_ERR_INVALID. Calls on one device share that scratch: calls that
+ * overlap on a device (two streams, two contexts, two threads) race. Not
+ * timed by mmhip_profile_*. f32 / f16 weights use no scratch. */
+#define MMHIP_NOALLOC_SCRATCH_BYTES 4456448u
+int mmhip_qmm_dev_noalloc(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat,
+                          const float* x_dev, float* y_dev, uint64_t batch,
+                          int out_layout);
+
 /* ======================================================================
  * MoE FFN layer: replaces moeFFN (src/inference.zig:886-1010) with
  * expertFFN (1152-1188), sharedExpertFFN (1094-1146), Scheduler.route

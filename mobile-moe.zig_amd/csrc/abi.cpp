@@ -8,6 +8,8 @@
 #include "../../include/mmhip.h"
 #include "backend.hpp"
 
+static_assert(MMHIP_NOALLOC_SCRATCH_BYTES == mmhip::kNoallocScratchBytes, "scratch size in the header and the library differ");
+
 namespace mmhip {
 const char* last_error_cstr();
 }
@@ -98,6 +100,14 @@ int mmhip_init(mmhip_ctx** out_ctx, int device) {
     if (e != hipSuccess) {
         delete ctx;
         return hip_fail(e, "init: hipStreamCreate");
+    }
+    // This device's address of the fixed scratch of mmhip_qmm_dev_noalloc,
+    // looked up once per device with the device current.
+    e = noalloc_scratch(device, &ctx->noalloc);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_fail(e, "init: scratch symbol address");
     }
     *out_ctx = ctx;
     return MMHIP_OK;
@@ -427,6 +437,39 @@ int mmhip_qmm_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const flo
     }
     std::lock_guard<std::mutex> lk(ctx->mu);
     return qmm_device(ctx, w, mat, x_dev, y_dev, batch, out_layout, &ctx->d_q);
+}
+
+int mmhip_qmm_dev_noalloc(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x_dev, float* y_dev,
+                          uint64_t batch, int out_layout) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!w || !x_dev || !y_dev || (out_layout != 0 && out_layout != 1)) {
+        set_error(MMHIP_ERR_INVALID, "qmm_dev_noalloc: null pointer or bad layout");
+        return MMHIP_ERR_INVALID;
+    }
+    if (batch == 0) return MMHIP_OK;
+    if (mat >= w->count) {
+        set_error(MMHIP_ERR_INVALID, "qmm_dev_noalloc: matrix index out of range");
+        return MMHIP_ERR_INVALID;
+    }
+    if (w->type == kF32 || w->type == kF16) {
+        // No scratch on this branch: the same launch as mmhip_qmm_dev.
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        return qmm_device(ctx, w, mat, x_dev, y_dev, batch, out_layout, nullptr);
+    }
+    const size_t need = quant_act_bytes(batch, w->geom.cols_pad);
+    if (need > MMHIP_NOALLOC_SCRATCH_BYTES) {
+        set_error(MMHIP_ERR_INVALID, "qmm_dev_noalloc: batch " + std::to_string(batch) + " x " +
+                                         std::to_string(w->geom.cols_pad) + " padded columns needs " +
+                                         std::to_string(need) + " bytes of scratch, above the fixed " +
+                                         std::to_string(MMHIP_NOALLOC_SCRATCH_BYTES));
+        return MMHIP_ERR_INVALID;
+    }
+    if (!ctx->noalloc) {
+        set_error(MMHIP_ERR_HIP, "qmm_dev_noalloc: no scratch address for this device");
+        return MMHIP_ERR_HIP;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    return qmm_quantised(ctx, w, mat, x_dev, y_dev, batch, out_layout, ctx->noalloc, false);
 }
 
 }  // extern "C"

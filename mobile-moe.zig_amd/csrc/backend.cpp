@@ -300,19 +300,28 @@ int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float*
                               (uint32_t)w->cols, ctx->stream);
         return e == hipSuccess ? MMHIP_OK : hip_fail(e, "qmm: launch");
     }
-    const TileGeom& g = w->geom;
-    e = qscratch->ensure(quant_act_bytes(batch, g.cols_pad));
+    e = qscratch->ensure(quant_act_bytes(batch, w->geom.cols_pad));
     if (e != hipSuccess) return hip_fail(e, "qmm: scratch");
-    QuantAct q = quant_act_view(qscratch->p, batch, g.cols_pad);
+    return qmm_quantised(ctx, w, mat, x, y, batch, out_layout, qscratch->p, true);
+}
+
+int qmm_quantised(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y, uint64_t batch,
+                  int out_layout, void* qbuf, bool timed) {
+    const TileGeom& g = w->geom;
+    // The quantiser writes every digit and scale of the batch x cols_pad
+    // block it reads back (columns past cols as zeros), so qbuf needs no
+    // clearing and keeps nothing from an earlier call.
+    const QuantAct q = quant_act_view(qbuf, batch, g.cols_pad);
+    hipError_t e;
     {
-        TimedLaunch tl(ctx, "quantize");
+        TimedLaunch tl(timed ? ctx : nullptr, "quantize");
         e = launch_quantize(x, w->cols, (uint32_t)batch, (uint32_t)w->cols, (uint32_t)g.cols_pad, q, ctx->stream,
                             g.fmt == kFmtIq2);
     }
     if (e != hipSuccess) return hip_fail(e, "qmm: quantize");
     const uint64_t ld = out_layout == 0 ? w->rows : batch;
     {
-        TimedLaunch tl(ctx, "qmm");
+        TimedLaunch tl(timed ? ctx : nullptr, "qmm");
         e = launch_group_dense(w->recs, w->dvals, g, mat, q, (uint32_t)batch, y, ld, out_layout, ctx->num_cu,
                                ctx->stream);
     }

@@ -81,6 +81,7 @@ struct mmhip_ctx {
     mmhip::DevBuf d_in, d_out, d_raw, d_q;
     mmhip::DevBuf d_arg;  // argmax partials (value, index) of the first pass
     mmhip::HostBuf h_in, h_out;
+    void* noalloc = nullptr;  // this device's fixed QMM scratch (mmhip_qmm_dev_noalloc)
     KernelTimer timer;
 };
 
@@ -89,11 +90,12 @@ struct TimedLaunch {
     mmhip_ctx* ctx;
     const char* family;
     hipEvent_t a = nullptr;
+    // A null ctx times nothing (callers that must not create events).
     TimedLaunch(mmhip_ctx* c, const char* f) : ctx(c), family(f) {
-        if (ctx->timer.on) ctx->timer.begin(ctx->stream, family, &a);
+        if (ctx && ctx->timer.on) ctx->timer.begin(ctx->stream, family, &a);
     }
     ~TimedLaunch() {
-        if (ctx->timer.on && a) ctx->timer.end(ctx->stream, family, a);
+        if (ctx && ctx->timer.on && a) ctx->timer.end(ctx->stream, family, a);
     }
 };
 
@@ -119,6 +121,11 @@ size_t quant_act_bytes(uint64_t n_vec, uint64_t cols_pad);
 // quantise x into `qscratch` first.
 int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t n, const float* x,
                 uint64_t x_stride, float* y, uint64_t y_stride, DevBuf* qscratch);
+// The quantised branch of qmm_device with the activation digits in `qbuf`
+// (at least quant_act_bytes(batch, cols_pad) bytes); allocates nothing and
+// records no timing events.
+int qmm_quantised(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y, uint64_t batch,
+                  int out_layout, void* qbuf, bool timed);
 int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y,
                uint64_t batch, int out_layout, DevBuf* qscratch);
 

@@ -133,6 +133,13 @@ hipError_t launch_gemv_q(const GemvArgs& a, uint32_t fmt, int num_cu, hipStream_
 // IQ2_XXS decode GEMV (gemv_iq2.hip); launch_gemv_q forwards IQ2_XXS here.
 hipError_t launch_gemv_iq2(const GemvArgs& a, int num_cu, hipStream_t s);
 
+// Allocation-free QMM scratch (noalloc.hip): kNoallocScratchBytes of device
+// memory per device, kept until the process ends. noalloc_scratch() returns
+// this device's address; call it with `device` current. Every call on a
+// device shares the same bytes.
+constexpr size_t kNoallocScratchBytes = 4456448;  // quantised activations of 256 vectors x 8192 columns
+hipError_t noalloc_scratch(int device, void** out);
+
 // Plain f32 / f16 weight GEMV (router, matVecMulUnified's f32 branch):
 // y_i = W_{first+i} . x_i for i < n_mats.
 hipError_t launch_gemv_float(const void* w, uint32_t ggml_type, uint64_t mat_stride,

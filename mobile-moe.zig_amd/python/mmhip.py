@@ -115,6 +115,7 @@ _SIGS = {
     "mmhip_gemv_batched_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _u64, _c_void_p, _u64,
                                               _c_void_p, _u64]),
     "mmhip_qmm_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _c_void_p, _u64, ctypes.c_int]),
+    "mmhip_qmm_dev_noalloc": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _c_void_p, _u64, ctypes.c_int]),
     "mmhip_moe_layer_create": (ctypes.c_int, [_c_void_p, ctypes.POINTER(MoeWeights), ctypes.POINTER(_c_void_p)]),
     "mmhip_moe_layer_destroy": (None, [_c_void_p, _c_void_p]),
     "mmhip_moe_ffn": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _u32,
@@ -371,6 +372,12 @@ class Context:
 
     def qmm_dev(self, w: Weight, mat: int, x: DeviceArray, y: DeviceArray, batch: int, out_layout: int = 0):
         check(self.lib.mmhip_qmm_dev(self.handle, w.handle, mat, x.ptr, y.ptr, batch, out_layout), "mmhip_qmm_dev")
+
+    def qmm_dev_noalloc(self, w: Weight, mat: int, x: DeviceArray, y: DeviceArray, batch: int, out_layout: int = 0):
+        """mmhip_qmm_dev_noalloc: the same product with the library's fixed
+        per-device scratch; allocates nothing."""
+        check(self.lib.mmhip_qmm_dev_noalloc(self.handle, w.handle, mat, x.ptr, y.ptr, batch, out_layout),
+              "mmhip_qmm_dev_noalloc")
 
     def dequantize_dev(self, out: DeviceArray, raw: DeviceArray, ggml_type: int, n: int):
         check(self.lib.mmhip_dequantize_dev(self.handle, out.ptr, raw.ptr, ggml_type, n), "mmhip_dequantize_dev")

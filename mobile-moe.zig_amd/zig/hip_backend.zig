@@ -147,6 +147,7 @@ extern fn mmhip_dequantize_dev(ctx: *Ctx, out_dev: ?*anyopaque, raw_dev: ?*const
 extern fn mmhip_gemv_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque) c_int;
 extern fn mmhip_gemv_batched_dev(ctx: *Ctx, w: *const Weight, first: u64, n_mats: u64, x_dev: ?*const anyopaque, x_stride: u64, y_dev: ?*anyopaque, y_stride: u64) c_int;
 extern fn mmhip_qmm_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque, batch: u64, out_layout: c_int) c_int;
+extern fn mmhip_qmm_dev_noalloc(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque, batch: u64, out_layout: c_int) c_int;
 extern fn mmhip_moe_layer_create(ctx: *Ctx, wts: *const MoeWeights, out_layer: *?*MoeLayerHandle) c_int;
 extern fn mmhip_moe_layer_destroy(ctx: *Ctx, layer: ?*MoeLayerHandle) void;
 extern fn mmhip_moe_ffn(ctx: *Ctx, layer: *MoeLayerHandle, hidden_host: [*]const f32, out_host: [*]f32, n_tokens: u32, rp: ?*const RouteParams, route_ids_host: ?[*]u32, route_weights_host: ?[*]f32) c_int;
@@ -245,6 +246,15 @@ pub const HipBackend = struct {
 
     /// sampleGreedy on device logits (e.g. computeLogits' GEMV output kept
     /// on the device); the id lands in device memory.
+    /// The batched QMM on device buffers with the library's fixed scratch:
+    /// allocates nothing, for code under graph capture or in loops that must
+    /// not allocate. No reference counterpart. batch x cols (rounded up to
+    /// 256) x 2.125 bytes must fit the 4,456,448-byte scratch; calls that
+    /// overlap on one device race.
+    pub fn qmmDevNoAlloc(self: *Self, w: *const Weight, mat: u64, x_dev: *const anyopaque, y_dev: *anyopaque, batch: u64, out_layout: c_int) !void {
+        try check(mmhip_qmm_dev_noalloc(self.ctx, w, mat, x_dev, y_dev, batch, out_layout));
+    }
+
     pub fn argmaxDev(self: *Self, out_dev: *anyopaque, logits_dev: *const anyopaque, n: u64) !void {
         try check(mmhip_argmax_dev(self.ctx, out_dev, logits_dev, n));
     }
