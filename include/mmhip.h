@@ -259,6 +259,26 @@ int mmhip_gemv_batched_dev(mmhip_ctx* ctx, const mmhip_weight* w,
                            uint64_t first, uint64_t n_mats,
                            const float* x_dev, uint64_t x_stride,
                            float* y_dev, uint64_t y_stride);
+/* Several mmhip_gemv_batched_dev calls in ONE launch: each group is a range
+ * of matrices of its own weight (weights may differ in shape, not in type;
+ * Q8_0 or IQ2_XXS), with its own inputs and outputs (strides in floats, 0
+ * shares one input vector). No counterpart in the reference: it issues the
+ * matVecMulUnified calls of a layer's experts (expertFFN,
+ * inference.zig:1171-1185), e.g. the routed experts' gate/up [1536 x 2048]
+ * and down [2048 x 1536] products of a step, as one launch instead of one per
+ * shape. IQ2_XXS results equal the separate calls' bit for bit; Q8_0 results
+ * agree to f32 rounding (a tile's record units may be split over the waves
+ * differently). */
+#define MMHIP_GEMV_MAX_GROUPS 4u
+typedef struct {
+    const mmhip_weight* w;
+    uint64_t first, n_mats;
+    const float* x_dev;
+    uint64_t x_stride;
+    float* y_dev;
+    uint64_t y_stride;
+} mmhip_gemv_group;
+int mmhip_gemv_grouped_dev(mmhip_ctx* ctx, const mmhip_gemv_group* groups, uint32_t n_groups);
 /* Batched QMM for prompt prefill: X [batch][cols] -> Y.
  * out_layout 0: Y [batch][rows] (batchMatMulUnified's layout);
  * out_layout 1: Y [rows][batch] (qmm.matMulQ8_0's layout, qmm.zig:52-57). */

@@ -9,6 +9,7 @@
 #include "backend.hpp"
 
 static_assert(MMHIP_NOALLOC_SCRATCH_BYTES == mmhip::kNoallocScratchBytes, "scratch size in the header and the library differ");
+static_assert(MMHIP_GEMV_MAX_GROUPS == mmhip::kGemvMaxSegs, "group limit in the header and the library differ");
 
 namespace mmhip {
 const char* last_error_cstr();
@@ -426,6 +427,44 @@ int mmhip_gemv_batched_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first
     }
     std::lock_guard<std::mutex> lk(ctx->mu);
     return gemv_device(ctx, w, first, n_mats, x_dev, x_stride, y_dev, y_stride, &ctx->d_q);
+}
+
+int mmhip_gemv_grouped_dev(mmhip_ctx* ctx, const mmhip_gemv_group* groups, uint32_t n_groups) {
+    if (int rc = require_ctx(ctx)) return rc;
+    if (!groups || n_groups == 0 || n_groups > MMHIP_GEMV_MAX_GROUPS) {
+        set_error(MMHIP_ERR_INVALID, "gemv_grouped_dev: need 1.." + std::to_string(MMHIP_GEMV_MAX_GROUPS) + " groups");
+        return MMHIP_ERR_INVALID;
+    }
+    GemvArgs segs[MMHIP_GEMV_MAX_GROUPS];
+    uint32_t fmt = 0;
+    for (uint32_t i = 0; i < n_groups; ++i) {
+        const mmhip_gemv_group& gr = groups[i];
+        if (!gr.w || !gr.x_dev || !gr.y_dev) {
+            set_error(MMHIP_ERR_INVALID, "gemv_grouped_dev: null pointer in group " + std::to_string(i));
+            return MMHIP_ERR_INVALID;
+        }
+        if (gr.w->type == kF32 || gr.w->type == kF16) {
+            set_error(MMHIP_ERR_UNSUPPORTED, "gemv_grouped_dev: quantised weights only (Q8_0, IQ2_XXS)");
+            return MMHIP_ERR_UNSUPPORTED;
+        }
+        if (gr.first + gr.n_mats > gr.w->count || gr.first + gr.n_mats < gr.first) {
+            set_error(MMHIP_ERR_INVALID, "gemv_grouped_dev: matrix range out of the weight in group " + std::to_string(i));
+            return MMHIP_ERR_INVALID;
+        }
+        if (i > 0 && gr.w->geom.fmt != fmt) {
+            set_error(MMHIP_ERR_INVALID, "gemv_grouped_dev: all groups must share one weight type");
+            return MMHIP_ERR_INVALID;
+        }
+        fmt = gr.w->geom.fmt;
+        segs[i] = gemv_args(gr.w, gr.first, gr.n_mats, gr.x_dev, gr.x_stride, gr.y_dev, gr.y_stride);
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipError_t e;
+    {
+        TimedLaunch tl(ctx, "gemv_q");
+        e = launch_gemv_segments(segs, n_groups, fmt, ctx->num_cu, ctx->stream);
+    }
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "gemv_grouped_dev: launch");
 }
 
 int mmhip_qmm_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x_dev, float* y_dev,

@@ -251,8 +251,18 @@ int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t 
         }
         return e == hipSuccess ? MMHIP_OK : hip_fail(e, "gemv: launch");
     }
-    const TileGeom& g = w->geom;
     (void)qscratch;
+    const GemvArgs a = gemv_args(w, first, n, x, x_stride, y, y_stride);
+    {
+        TimedLaunch tl(ctx, "gemv_q");
+        e = launch_gemv_q(a, w->geom.fmt, ctx->num_cu, ctx->stream);
+    }
+    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "gemv: launch");
+}
+
+GemvArgs gemv_args(const mmhip_weight* w, uint64_t first, uint64_t n, const float* x, uint64_t x_stride, float* y,
+                   uint64_t y_stride) {
+    const TileGeom& g = w->geom;
     GemvArgs a{};
     a.recs = w->recs;
     a.dvals = w->dvals;
@@ -274,11 +284,7 @@ int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t 
     a.rows = (uint32_t)g.rows;
     a.cols = (uint32_t)g.cols;
     a.tiles_per_wg = 0;
-    {
-        TimedLaunch tl(ctx, "gemv_q");
-        e = launch_gemv_q(a, g.fmt, ctx->num_cu, ctx->stream);
-    }
-    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "gemv: launch");
+    return a;
 }
 
 int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y, uint64_t batch,

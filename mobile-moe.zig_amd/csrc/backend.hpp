@@ -126,6 +126,10 @@ int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t 
 // records no timing events.
 int qmm_quantised(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y, uint64_t batch,
                   int out_layout, void* qbuf, bool timed);
+// Kernel arguments of a GEMV over matrices [first, first + n) of a quantised
+// weight (x_i = x + i * x_stride, y_i = y + i * y_stride).
+GemvArgs gemv_args(const mmhip_weight* w, uint64_t first, uint64_t n, const float* x, uint64_t x_stride, float* y,
+                   uint64_t y_stride);
 int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y,
                uint64_t batch, int out_layout, DevBuf* qscratch);
 

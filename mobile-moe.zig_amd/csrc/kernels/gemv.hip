@@ -55,8 +55,8 @@ struct StepPos {
 // in flight while LDS is filled. The stream runs one step ahead (two register
 // buffers): the CU's queue holds about one step per wave, and a deeper
 // prefetch only blocks the issuing wave.
-template <int UPS, int WG, int DEPTH, bool ROUTE>
-__global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
+template <int UPS, int WG, int DEPTH, bool ROUTE, int NSEG>
+__global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set) {
     constexpr int FMT = kFmtQ8;
     constexpr uint32_t kWaves = WG / 64;
     constexpr int kRing = DEPTH + 1;  // register buffers: the step computing + DEPTH in flight
@@ -64,6 +64,14 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     __shared__ float row_sum[kGemvMaxTiles * 16];
     __shared__ float edge[2][kWaves * 16];
     extern __shared__ __align__(16) uint8_t smem[];
+    // This workgroup's segment and problem within it.
+    uint32_t si = 0;
+#pragma unroll
+    for (int q = 1; q < NSEG; ++q)
+        if (blockIdx.y >= set.y_begin[q]) si = q;
+    const GemvArgs& a = set.seg[si];
+    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
+    if (t_begin >= a.tiles) return;  // whole workgroup: the grid is sized for the widest segment
     constexpr uint32_t kBlkPerUnit = 2;
     const uint32_t nblk_all = a.units * kBlkPerUnit;
     const uint32_t chunk_blk = nblk_all < kChunkBlocks ? nblk_all : kChunkBlocks;
@@ -73,7 +81,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t p = blockIdx.y;
+    const uint32_t p = blockIdx.y - set.y_begin[si];
     uint64_t mat = a.first_mat + p, x_row = p, y_row = p;
     if constexpr (ROUTE) {
         // Every wave routes the token (same result); the problem follows.
@@ -108,7 +116,6 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvArgs a) {
     const float* x = a.x + x_row * a.x_stride;
     float* const y_base = a.y + y_row * a.y_stride;
     const bool silu_mul = a.silu_mul != 0;
-    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;  // < a.tiles (grid size)
     const uint32_t n_tiles = min(a.tiles - t_begin, a.tiles_per_wg);
     const bool has_a = n < 2;
     const int8_t* a_run = aq + (n & 1) * 4 * kARun + g * kARun;  // used by lanes n < 2 only
@@ -383,10 +390,10 @@ static int pick_ups(uint32_t units) {
     return 0;
 }
 
-template <int WG, int DEPTH, bool ROUTE>
+template <int WG, int DEPTH, bool ROUTE, int NSEG>
 static const void* kernel_for(int ups) {
-    return ups == 8 ? reinterpret_cast<const void*>(&gemv_q_kernel<8, WG, DEPTH, ROUTE>)
-                    : reinterpret_cast<const void*>(&gemv_q_kernel<4, WG, DEPTH, ROUTE>);
+    return ups == 8 ? reinterpret_cast<const void*>(&gemv_q_kernel<8, WG, DEPTH, ROUTE, NSEG>)
+                    : reinterpret_cast<const void*>(&gemv_q_kernel<4, WG, DEPTH, ROUTE, NSEG>);
 }
 
 static int env_int(const char* name, int dflt) {
@@ -396,14 +403,43 @@ static int env_int(const char* name, int dflt) {
 
 template <int DEPTH>
 static const void* kernel_for_wg(int wg, int ups) {
-    if (wg == 1024) return kernel_for<1024, DEPTH, false>(ups);
-    return kernel_for<256, DEPTH, false>(ups);
+    if (wg == 1024) return kernel_for<1024, DEPTH, false, 1>(ups);
+    return kernel_for<256, DEPTH, false, 1>(ups);
 }
 
-hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStream_t s) {
-    if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
-    if (fmt == kFmtIq2) return launch_gemv_iq2(a_in, num_cu, s);
-    GemvArgs a = a_in;
+template <int N>
+static hipError_t launch_q_set(const GemvArgs* segs, uint32_t n_segs, const void* fn, uint32_t grid_x, int wg,
+                               size_t lds, hipStream_t s) {
+    GemvSet<N> set{};
+    uint32_t y = 0;
+    for (uint32_t i = 0; i < (uint32_t)N; ++i) {
+        if (i < n_segs) {
+            set.seg[i] = segs[i];
+            set.y_begin[i] = y;
+            y += segs[i].n_probs;
+        } else {
+            set.seg[i] = segs[0];
+            set.y_begin[i] = 0xFFFFFFFFu;  // never selected
+        }
+    }
+    void* args[] = {&set};
+    return hipLaunchKernel(fn, dim3(grid_x, y), dim3(wg), args, lds, s);
+}
+
+hipError_t launch_gemv_q(const GemvArgs& a, uint32_t fmt, int num_cu, hipStream_t s) {
+    return launch_gemv_segments(&a, 1, fmt, num_cu, s);
+}
+
+hipError_t launch_gemv_segments(const GemvArgs* segs_in, uint32_t n_segs, uint32_t fmt, int num_cu, hipStream_t s) {
+    if (n_segs == 0 || n_segs > kGemvMaxSegs) return hipErrorInvalidValue;
+    if (fmt == kFmtIq2) return launch_gemv_iq2(segs_in, n_segs, num_cu, s);
+    GemvArgs segs[kGemvMaxSegs];
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < n_segs; ++i)
+        if (segs_in[i].n_probs && segs_in[i].tiles) segs[n++] = segs_in[i];
+    if (n == 0) return hipSuccess;
+    const bool route = segs[0].route_decode != 0;
+    if (route && n != 1) return hipErrorInvalidValue;
     // Defaults measured on MI355X with 64-matrix batches: 256 threads, one
     // workgroup per CU, two steps of 4 units in flight: four long streams
     // per CU keep fewer requests outstanding and reach a higher HBM rate than
@@ -412,33 +448,56 @@ hipError_t launch_gemv_q(const GemvArgs& a_in, uint32_t fmt, int num_cu, hipStre
     static const int wg_env = env_int("MMHIP_GEMV_WG", 0);
     static const int cap_env = env_int("MMHIP_GEMV_MAX_UPS", 0);
     static const int depth_env = env_int("MMHIP_GEMV_DEPTH", 0);
-    const int wg = wg_env == 1024 ? 1024 : 256;
+    const int wg = wg_env == 1024 && n == 1 ? 1024 : 256;
     // Steps above 4 units exceed the register budget with two record
-    // buffers in flight and spill.
+    // buffers in flight and spill. A step size must divide every segment's
+    // tile and chunk unit counts.
     const int cap = cap_env == 8 ? 8 : 4;
-    int ups = pick_ups(a.units);
-    if (ups == 0) return hipErrorInvalidValue;
-    if (ups > cap) ups = cap;
-    const int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : 2;
-    const void* fn;
-    if (a.route_decode) {
-        // Decode gate/up with routing in the kernel: the default shape only.
-        fn = kernel_for<256, 2, true>(ups);
-    } else {
-        fn = depth == 1 ? kernel_for_wg<1>(wg, ups) : depth == 3 ? kernel_for_wg<3>(wg, ups) : kernel_for_wg<2>(wg, ups);
+    int ups = cap;
+    size_t lds = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        int u = pick_ups(segs[i].units);
+        if (u == 0) return hipErrorInvalidValue;
+        if (u < ups) ups = u;
+        const size_t l = gemv_q_lds_bytes(segs[i].units);
+        if (l > lds) lds = l;
     }
-    const size_t lds = gemv_q_lds_bytes(a.units);
     // Tiles per workgroup: the problems' tiles spread over one workgroup per
-    // CU, at most kGemvMaxTiles (the LDS row sums).
-    const uint64_t total_tiles = (uint64_t)a.n_probs * a.tiles;
+    // CU (several segments: about the same record units per workgroup), at
+    // most kGemvMaxTiles (the LDS row sums).
     const uint64_t target_wgs = (uint64_t)(num_cu > 0 ? num_cu : 256);
-    uint64_t tpw = (total_tiles + target_wgs - 1) / target_wgs;
-    if (tpw > kGemvMaxTiles) tpw = kGemvMaxTiles;
-    if (tpw > a.tiles) tpw = a.tiles;
-    a.tiles_per_wg = (uint32_t)tpw;
-    dim3 grid((unsigned)((a.tiles + tpw - 1) / tpw), a.n_probs);
-    void* args[] = {&a};
-    return hipLaunchKernel(fn, grid, dim3(wg), args, lds, s);
+    uint32_t grid_x = 1;
+    if (n == 1) {
+        GemvArgs& a = segs[0];
+        uint64_t tpw = ((uint64_t)a.n_probs * a.tiles + target_wgs - 1) / target_wgs;
+        if (tpw > kGemvMaxTiles) tpw = kGemvMaxTiles;
+        if (tpw > a.tiles) tpw = a.tiles;
+        a.tiles_per_wg = (uint32_t)tpw;
+        grid_x = (a.tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
+    } else {
+        uint64_t units = 0;
+        for (uint32_t i = 0; i < n; ++i) units += (uint64_t)segs[i].n_probs * segs[i].tiles * segs[i].units;
+        const uint64_t per_wg = (units + target_wgs - 1) / target_wgs;
+        for (uint32_t i = 0; i < n; ++i) {
+            GemvArgs& a = segs[i];
+            uint64_t t = (per_wg + a.units - 1) / a.units;
+            if (t > kGemvMaxTiles) t = kGemvMaxTiles;
+            if (t > a.tiles) t = a.tiles;
+            if (t < 1) t = 1;
+            a.tiles_per_wg = (uint32_t)t;
+            const uint32_t gx = (a.tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
+            if (gx > grid_x) grid_x = gx;
+        }
+    }
+    const int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : 2;
+    if (route) return launch_q_set<1>(segs, 1, kernel_for<256, 2, true, 1>(ups), grid_x, 256, lds, s);
+    if (n == 1) {
+        const void* fn =
+            depth == 1 ? kernel_for_wg<1>(wg, ups) : depth == 3 ? kernel_for_wg<3>(wg, ups) : kernel_for_wg<2>(wg, ups);
+        return launch_q_set<1>(segs, 1, fn, grid_x, wg, lds, s);
+    }
+    if (n == 2) return launch_q_set<2>(segs, 2, kernel_for<256, 2, false, 2>(ups), grid_x, 256, lds, s);
+    return launch_q_set<4>(segs, n, kernel_for<256, 2, false, 4>(ups), grid_x, 256, lds, s);
 }
 
 hipError_t launch_gemv_float(const void* w, uint32_t type, uint64_t mat_stride, const float* x,

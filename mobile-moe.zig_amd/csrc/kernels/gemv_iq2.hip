@@ -3,7 +3,9 @@
 // inference.zig:1171-1185, without the f32 dequantization round trip).
 //
 // One 1024-thread workgroup per CU owns one problem (matrix + activation
-// vector) and up to kQMaxTiles 16-row tiles. The activation is quantised into
+// vector) and up to kQMaxTiles 16-row tiles (kQMaxItems record units per
+// activation chunk). A launch may hold several segments (weights of
+// different shapes), each owning a range of the grid's problem rows. The activation is quantised into
 // LDS per K-chunk of up to 8 record units (2048 columns) as two int8 digit
 // planes per 32-column block (x ~ s (256 hi + lo)).
 //
@@ -23,8 +25,8 @@
 // sub-blocks whose ls bits its own record dwords carry.
 //
 // B operands come from the 32 KiB LDS table keyed by b012 | P | idx (record
-// layout in device_common.hpp); the hi3 signs of the high dword are applied
-// in registers (iq2_fix_hi). The table reads of both items of a pair are
+// layout in device_common.hpp); the hi3 signs of the high dword come from an
+// 8-entry mask table and are applied with one xor-add. The table reads of both items of a pair are
 // issued before either is used.
 //
 // Each item leaves its 64 lane partial sums in LDS; after a chunk, every
@@ -42,7 +44,8 @@ constexpr int kQWg = 1024;
 constexpr uint32_t kQWaves = kQWg / 64;
 constexpr uint32_t kQChunkUnits = 8;                 // record units per activation chunk
 constexpr uint32_t kQChunkBlocks = kQChunkUnits * 8;  // 32-column blocks per chunk
-constexpr uint32_t kQMaxTiles = 48;                  // row tiles per workgroup
+constexpr uint32_t kQMaxTiles = 64;                  // row tiles per workgroup
+constexpr uint32_t kQMaxItems = 384;                 // (unit, tile) items per workgroup and chunk
 
 // Quantises 4 columns per lane (8 lanes per 32-column block, quantize_quad)
 // into the chunk's digit planes: aq[(b * 2 + digit) * 32 + column].
@@ -121,31 +124,38 @@ struct ItemPos {
 };
 
 // Raw table words of one record unit (lane's 8 records): .x = low dword,
-// .y = high dword before the hi3 signs.
+// .y = high dword before the hi3 signs; m: the hi3 sign masks (0xFF in each
+// byte to negate).
 struct RawB {
     uint2 e[8];
+    uint32_t m[8];
 };
 
 // Table words of the lane's 8 records (record layout in device_common.hpp):
 // the 8-byte entry keyed by the record's window; its high dword still needs
 // the hi3 signs.
-__device__ __forceinline__ void fetch_b(const uint4& r, const uint32_t* tab, RawB& raw) {
+// The masks (one dword per hi3 value) are read from an 8-entry table: 64 lanes touch at most 8 addresses in 16 banks, so these
+// reads are broadcasts without bank conflicts, and they replace the four
+// VALU instructions that would build each mask.
+__device__ __forceinline__ void fetch_b(const uint4& r, const uint32_t* tab, const uint32_t* mtab, RawB& raw) {
     const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
     const char* t8 = reinterpret_cast<const char*>(tab);
+    const char* m8 = reinterpret_cast<const char*>(mtab);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         const uint32_t d = w4[s >> 1];
         raw.e[s] = *reinterpret_cast<const uint2*>(t8 + ((s & 1) ? ((d >> 15) & 0x7FF8u) : (d & 0x7FF8u)));
+        // hi3 of sub-block 2k + 1: bits 0..2; of 2k: bits 15..17 (times 4 bytes).
+        raw.m[s] = *reinterpret_cast<const uint32_t*>(m8 + (((s & 1) ? (d << 2) : (d >> 13)) & 0x1Cu));
     }
 }
 
 // B operands (signed int8 weights, 8 per record) from the table words.
-__device__ __forceinline__ void finish_b(const uint4& r, const RawB& raw, long (&b)[8]) {
-    const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+__device__ __forceinline__ void finish_b(const RawB& raw, long (&b)[8]) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        const uint32_t d = w4[s >> 1];
-        const uint32_t hi = iq2_fix_hi(raw.e[s].y, (s & 1) ? (d & 7u) : ((d >> 15) & 7u));
+        // Bytes (b ^ 0xFF) + 1 = -b where the mask is set (|b| <= 0x2B: no carry).
+        const uint32_t hi = negate_bytes(raw.e[s].y, raw.m[s]);
         b[s] = (long)(((uint64_t)hi << 32) | (uint64_t)raw.e[s].x);
     }
 }
@@ -158,14 +168,15 @@ __device__ __forceinline__ v4i bpair(const long (&b)[8], int j) {
     return v4i{(int)(uint32_t)l, (int)(uint32_t)(l >> 32), (int)(uint32_t)h, (int)(uint32_t)(h >> 32)};
 }
 
-template <int DEPTH, bool ROUTE>
-__global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
+template <int DEPTH, bool ROUTE, int NSEG>
+__global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     constexpr int kRing = DEPTH + 1;
     // One LDS block with the table first: its byte offsets (below 32 KiB)
     // fold into the ds_read offset fields.
     struct Lds {
         uint32_t tab[kIq2TableWords];
-        float part[kQChunkUnits * kQMaxTiles * 64];
+        uint32_t mtab[8];  // hi3 sign masks
+        float part[kQMaxItems * 64];
         uint8_t aq[kQChunkBlocks * 64];
         float xs[kQChunkBlocks];
         float row_sum[kQMaxTiles * 16];
@@ -173,10 +184,21 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
     };
     __shared__ __align__(16) Lds lds;
     uint32_t* const tab = lds.tab;
+    const uint32_t* const mtab = lds.mtab;
     float* const part = lds.part;
     uint8_t* const aq = lds.aq;
     float* const xs = lds.xs;
     float* const row_sum = lds.row_sum;
+
+    // This workgroup's segment and problem within it.
+    uint32_t si = 0;
+#pragma unroll
+    for (int q = 1; q < NSEG; ++q)
+        if (blockIdx.y >= set.y_begin[q]) si = q;
+    const GemvArgs& a = set.seg[si];
+    const uint32_t py = blockIdx.y - set.y_begin[si];
+    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
+    if (t_begin >= a.tiles) return;  // whole workgroup: the grid is sized for the widest segment
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t n = lane & 15, g = lane >> 4;
@@ -187,12 +209,11 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
     // wave: sixteen waves routing the same token cost ~2 us of issue time).
     uint64_t mat = 0, x_row = 0, y_row = 0;
     if constexpr (!ROUTE) {
-        if (!select_problem<false>(a, blockIdx.y, mat, x_row, y_row)) return;  // whole workgroup
+        if (!select_problem<false>(a, py, mat, x_row, y_row)) return;  // whole workgroup
     }
     const float* x = a.x + x_row * a.x_stride;
     float* y_base = nullptr;
     const bool silu_mul = a.silu_mul != 0;
-    const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;  // < a.tiles (grid size)
     const uint32_t n_tiles = min(a.tiles - t_begin, a.tiles_per_wg);
     BufRsrc rec_r, d_r;
     const uint32_t rec_voff = lane * 16;
@@ -263,7 +284,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
             // through LDS; the barrier also orders every wave's loads above
             // before its weight loads.
             if (wave == 0) {
-                const bool run = select_problem<true>(a, blockIdx.y, mat, x_row, y_row);
+                const bool run = select_problem<true>(a, py, mat, x_row, y_row);
                 if (lane == 0) {
                     lds.sel[0] = run ? (uint32_t)mat : ~0u;
                     lds.sel[1] = (uint32_t)y_row;
@@ -283,6 +304,11 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
         issue_first();
 #pragma unroll
         for (int i = 0; i < 2; ++i) reinterpret_cast<uint4*>(tab)[threadIdx.x + kQWg * i] = tv[i];
+        if (threadIdx.x < 8) {
+            // Columns 4..6 take hi3's bits, column 7 its parity (the ksigns
+            // parity bit; column 7's P sign is already in the table word).
+            lds.mtab[threadIdx.x] = nibble_byte_mask(threadIdx.x | (parity3(threadIdx.x) << 3));
+        }
         for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += kQWg) row_sum[i] = 0.0f;
         if (silu_mul) silu_mul4(xv, uv);
         x_store_planes(xv, nb, 0, aq, xs);  // one pass covers 128 >= 64 blocks
@@ -317,11 +343,11 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
                     }
                     // B operands of both items: all table reads first.
                     RawB raw0, raw1;
-                    fetch_b(rb[q][0], tab, raw0);
-                    fetch_b(rb[q][1], tab, raw1);
+                    fetch_b(rb[q][0], tab, mtab, raw0);
+                    fetch_b(rb[q][1], tab, mtab, raw1);
                     long b0[8], b1[8];
-                    finish_b(rb[q][0], raw0, b0);
-                    finish_b(rb[q][1], raw1, b1);
+                    finish_b(raw0, b0);
+                    finish_b(raw1, b1);
                     v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -376,49 +402,102 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvArgs a) {
     }
 }
 
-template <int DEPTH>
-static const void* iq2_kernel_for(bool route) {
-    return route ? reinterpret_cast<const void*>(&gemv_iq2_kernel<DEPTH, true>)
-                 : reinterpret_cast<const void*>(&gemv_iq2_kernel<DEPTH, false>);
-}
-
 static int env_int(const char* name, int dflt) {
     const char* e = getenv(name);
     return e ? atoi(e) : dflt;
 }
 
-}  // namespace
+// Largest tiles per workgroup for a segment: the LDS holds kQMaxTiles row
+// sums and kQMaxItems (unit, tile) partials per activation chunk.
+static uint32_t max_tiles_per_wg(const GemvArgs& a) {
+    const uint32_t uc = a.units < kQChunkUnits ? a.units : kQChunkUnits;
+    uint32_t m = kQMaxItems / uc;
+    if (m > kQMaxTiles) m = kQMaxTiles;
+    return a.tiles < m ? a.tiles : m;
+}
 
-hipError_t launch_gemv_iq2(const GemvArgs& a_in, int num_cu, hipStream_t s) {
-    if (a_in.n_probs == 0 || a_in.tiles == 0) return hipSuccess;
-    GemvArgs a = a_in;
-    // Pairs in flight per wave: 2 (measured best), MMHIP_IQ2_DEPTH=3 to override.
-    static const int depth_env = env_int("MMHIP_IQ2_DEPTH", 0);
-    const bool route = a.route_decode != 0;
-    const void* fn = (depth_env == 3 && !route) ? iq2_kernel_for<3>(false) : iq2_kernel_for<2>(route);
-    // Tiles per workgroup (at most kQMaxTiles: the LDS partials and row
-    // sums). One workgroup fits a CU, so a grid of W workgroups runs in
-    // ceil(W / CUs) rounds; the choice minimises rounds x (tiles x units x
-    // per-item time + per-workgroup fixed time), with the costs measured on
-    // MI355X (~65 ns per 1 KiB item per CU, ~2 us of prologue and tail).
-    // E.g. 10 matrices of 128 tiles take 6 tiles per workgroup (220
-    // workgroups, one round) rather than 5 (260, two rounds).
-    const uint64_t cus = (uint64_t)(num_cu > 0 ? num_cu : 256);
-    const uint32_t max_tpw = a.tiles < kQMaxTiles ? a.tiles : kQMaxTiles;
-    uint32_t tpw = max_tpw;
-    double best = 0.0;
-    for (uint32_t t = 1; t <= max_tpw; ++t) {
-        const uint64_t wgs = (uint64_t)a.n_probs * ((a.tiles + t - 1) / t);
-        const double cost = (double)((wgs + cus - 1) / cus) * ((double)t * a.units * 0.065 + 2.0);
-        if (t == 1 || cost < best) {
-            best = cost;
-            tpw = t;
+template <int N>
+static hipError_t launch_set(const GemvArgs* segs, uint32_t n_segs, const void* fn, uint32_t grid_x, hipStream_t s) {
+    GemvSet<N> set{};
+    uint32_t y = 0;
+    for (uint32_t i = 0; i < (uint32_t)N; ++i) {
+        if (i < n_segs) {
+            set.seg[i] = segs[i];
+            set.y_begin[i] = y;
+            y += segs[i].n_probs;
+        } else {
+            set.seg[i] = segs[0];
+            set.y_begin[i] = 0xFFFFFFFFu;  // never selected
         }
     }
-    a.tiles_per_wg = tpw;
-    dim3 grid((unsigned)((a.tiles + tpw - 1) / tpw), a.n_probs);
-    void* args[] = {&a};
-    return hipLaunchKernel(fn, grid, dim3(kQWg), args, 0, s);
+    void* args[] = {&set};
+    return hipLaunchKernel(fn, dim3(grid_x, y), dim3(kQWg), args, 0, s);
+}
+
+}  // namespace
+
+hipError_t launch_gemv_iq2(const GemvArgs* segs_in, uint32_t n_segs, int num_cu, hipStream_t s) {
+    if (n_segs == 0 || n_segs > kGemvMaxSegs) return hipErrorInvalidValue;
+    GemvArgs segs[kGemvMaxSegs];
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < n_segs; ++i)
+        if (segs_in[i].n_probs && segs_in[i].tiles) segs[n++] = segs_in[i];
+    if (n == 0) return hipSuccess;
+    const bool route = segs[0].route_decode != 0;
+    if (route && n != 1) return hipErrorInvalidValue;
+    const uint64_t cus = (uint64_t)(num_cu > 0 ? num_cu : 256);
+    uint32_t grid_x = 1;
+    if (n == 1) {
+        // Tiles per workgroup. One workgroup fits a CU, so a grid of W
+        // workgroups runs in ceil(W / CUs) rounds; the choice minimises
+        // rounds x (tiles x units x per-item time + per-workgroup fixed
+        // time), with the costs measured on MI355X (~65 ns per 1 KiB item
+        // per CU, ~2 us of prologue and tail). E.g. 10 matrices of 128 tiles
+        // take 6 tiles per workgroup (220 workgroups, one round) rather than
+        // 5 (260, two rounds).
+        GemvArgs& a = segs[0];
+        const uint32_t max_tpw = max_tiles_per_wg(a);
+        uint32_t tpw = max_tpw;
+        double best = 0.0;
+        for (uint32_t t = 1; t <= max_tpw; ++t) {
+            const uint64_t wgs = (uint64_t)a.n_probs * ((a.tiles + t - 1) / t);
+            const double cost = (double)((wgs + cus - 1) / cus) * ((double)t * a.units * 0.065 + 2.0);
+            if (t == 1 || cost < best) {
+                best = cost;
+                tpw = t;
+            }
+        }
+        a.tiles_per_wg = tpw;
+        grid_x = (a.tiles + tpw - 1) / tpw;
+    } else {
+        // Several segments: every workgroup gets about the same number of
+        // items (the total over the CUs), so the whole launch is one round
+        // when the segments allow it.
+        uint64_t items = 0;
+        for (uint32_t i = 0; i < n; ++i) items += (uint64_t)segs[i].n_probs * segs[i].tiles * segs[i].units;
+        const uint64_t per_wg = (items + cus - 1) / cus;
+        for (uint32_t i = 0; i < n; ++i) {
+            GemvArgs& a = segs[i];
+            uint64_t t = (per_wg + a.units - 1) / a.units;
+            const uint32_t m = max_tiles_per_wg(a);
+            if (t > m) t = m;
+            if (t < 1) t = 1;
+            a.tiles_per_wg = (uint32_t)t;
+            const uint32_t gx = (a.tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
+            if (gx > grid_x) grid_x = gx;
+        }
+    }
+    // Pairs in flight per wave: 2 (measured best), MMHIP_IQ2_DEPTH=3 to override.
+    static const int depth_env = env_int("MMHIP_IQ2_DEPTH", 0);
+    if (route) return launch_set<1>(segs, 1, reinterpret_cast<const void*>(&gemv_iq2_kernel<2, true, 1>), grid_x, s);
+    if (n == 1) {
+        const void* fn = depth_env == 3 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 1>)
+                                        : reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 1>);
+        return launch_set<1>(segs, 1, fn, grid_x, s);
+    }
+    if (n == 2)
+        return launch_set<2>(segs, 2, reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 2>), grid_x, s);
+    return launch_set<4>(segs, n, reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 4>), grid_x, s);
 }
 
 }  // namespace mmhip

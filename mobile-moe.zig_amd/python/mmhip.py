@@ -47,6 +47,11 @@ class RouteParams(ctypes.Structure):
                 ("deferral_bias_host", _fp)]
 
 
+class GemvGroup(ctypes.Structure):
+    _fields_ = [("w", _c_void_p), ("first", _u64), ("n_mats", _u64), ("x_dev", _c_void_p), ("x_stride", _u64),
+                ("y_dev", _c_void_p), ("y_stride", _u64)]
+
+
 class Shape(ctypes.Structure):
     _fields_ = [("m", _u32), ("n", _u32), ("k", _u32), ("dim", _u32)]
 
@@ -112,6 +117,7 @@ _SIGS = {
     "mmhip_quantize_q8_0_rows_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _u64, _u64, _u32]),
     "mmhip_dequantize_q8_0_rows_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _u64, _u32]),
     "mmhip_gemv_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _c_void_p]),
+    "mmhip_gemv_grouped_dev": (ctypes.c_int, [_c_void_p, ctypes.POINTER(GemvGroup), _u32]),
     "mmhip_gemv_batched_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _u64, _c_void_p, _u64,
                                               _c_void_p, _u64]),
     "mmhip_qmm_dev": (ctypes.c_int, [_c_void_p, _c_void_p, _u64, _c_void_p, _c_void_p, _u64, ctypes.c_int]),
@@ -369,6 +375,21 @@ class Context:
                          y_stride: int):
         check(self.lib.mmhip_gemv_batched_dev(self.handle, w.handle, first, n, x.ptr, x_stride, y.ptr, y_stride),
               "mmhip_gemv_batched_dev")
+
+    def gemv_groups(self, groups) -> ctypes.Array:
+        """groups: (weight, first, n_mats, x, x_stride, y, y_stride) tuples ->
+        the mmhip_gemv_group array mmhip_gemv_grouped_dev takes (built once,
+        reusable)."""
+        arr = (GemvGroup * len(groups))()
+        for i, (w, first, n, x, xs, y, ys) in enumerate(groups):
+            arr[i] = GemvGroup(w.handle, first, n, x.ptr, xs, y.ptr, ys)
+        return arr
+
+    def gemv_grouped_dev(self, groups):
+        """mmhip_gemv_grouped_dev: several GEMV groups (tuples as gemv_groups,
+        or its array) in one launch."""
+        arr = groups if isinstance(groups, ctypes.Array) else self.gemv_groups(groups)
+        check(self.lib.mmhip_gemv_grouped_dev(self.handle, arr, len(arr)), "mmhip_gemv_grouped_dev")
 
     def qmm_dev(self, w: Weight, mat: int, x: DeviceArray, y: DeviceArray, batch: int, out_layout: int = 0):
         check(self.lib.mmhip_qmm_dev(self.handle, w.handle, mat, x.ptr, y.ptr, batch, out_layout), "mmhip_qmm_dev")

@@ -14,6 +14,7 @@
 const std = @import("std");
 const gguf = @import("gguf.zig");
 const dequant = @import("dequant.zig");
+const scheduler = @import("scheduler.zig");
 
 // ---- C ABI (include/mmhip.h) ----
 
@@ -44,6 +45,16 @@ pub const RouteParams = extern struct {
     throttle_level: i32 = 0,
     active_expert_limit: u32 = 0,
     deferral_bias_host: ?[*]const f32 = null,
+};
+
+pub const GemvGroup = extern struct {
+    w: ?*const Weight,
+    first: u64,
+    n_mats: u64,
+    x_dev: ?[*]const f32,
+    x_stride: u64,
+    y_dev: ?[*]f32,
+    y_stride: u64,
 };
 
 pub const Shape = extern struct { m: u32 = 0, n: u32 = 0, k: u32 = 0, dim: u32 = 0 };
@@ -139,19 +150,20 @@ extern fn mmhip_batch_mat_mul(ctx: *Ctx, out_host: [*]f32, ptr_host: ?*const any
 extern fn mmhip_dequantize(ctx: *Ctx, out_host: [*]f32, data_host: ?*const anyopaque, type_: u32, n_elements: u64) c_int;
 extern fn mmhip_forget(ctx: *Ctx, ptr_host: ?*const anyopaque) c_int;
 extern fn mmhip_sample_greedy(ctx: *Ctx, out_host: *u32, logits_host: [*]const f32, n: u64) c_int;
-extern fn mmhip_argmax_dev(ctx: *Ctx, out_dev: ?*anyopaque, logits_dev: ?*const anyopaque, n: u64) c_int;
+extern fn mmhip_argmax_dev(ctx: *Ctx, out_dev: ?*u32, logits_dev: ?[*]const f32, n: u64) c_int;
 extern fn mmhip_quantize_q8_0(ctx: *Ctx, blocks_host: ?*anyopaque, x_host: [*]const f32, n_elements: u64) c_int;
-extern fn mmhip_quantize_q8_0_rows_dev(ctx: *Ctx, blocks_dev: ?*anyopaque, x_dev: ?*const anyopaque, x_stride: u64, n_rows: u64, row_len: u32) c_int;
-extern fn mmhip_dequantize_q8_0_rows_dev(ctx: *Ctx, out_dev: ?*anyopaque, out_stride: u64, blocks_dev: ?*const anyopaque, n_rows: u64, row_len: u32) c_int;
-extern fn mmhip_dequantize_dev(ctx: *Ctx, out_dev: ?*anyopaque, raw_dev: ?*const anyopaque, type_: u32, n_elements: u64) c_int;
-extern fn mmhip_gemv_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque) c_int;
-extern fn mmhip_gemv_batched_dev(ctx: *Ctx, w: *const Weight, first: u64, n_mats: u64, x_dev: ?*const anyopaque, x_stride: u64, y_dev: ?*anyopaque, y_stride: u64) c_int;
-extern fn mmhip_qmm_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque, batch: u64, out_layout: c_int) c_int;
-extern fn mmhip_qmm_dev_noalloc(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?*const anyopaque, y_dev: ?*anyopaque, batch: u64, out_layout: c_int) c_int;
+extern fn mmhip_quantize_q8_0_rows_dev(ctx: *Ctx, blocks_dev: ?*anyopaque, x_dev: ?[*]const f32, x_stride: u64, n_rows: u64, row_len: u32) c_int;
+extern fn mmhip_dequantize_q8_0_rows_dev(ctx: *Ctx, out_dev: ?[*]f32, out_stride: u64, blocks_dev: ?*const anyopaque, n_rows: u64, row_len: u32) c_int;
+extern fn mmhip_dequantize_dev(ctx: *Ctx, out_dev: ?[*]f32, raw_dev: ?*const anyopaque, type_: u32, n_elements: u64) c_int;
+extern fn mmhip_gemv_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?[*]const f32, y_dev: ?[*]f32) c_int;
+extern fn mmhip_gemv_batched_dev(ctx: *Ctx, w: *const Weight, first: u64, n_mats: u64, x_dev: ?[*]const f32, x_stride: u64, y_dev: ?[*]f32, y_stride: u64) c_int;
+extern fn mmhip_gemv_grouped_dev(ctx: *Ctx, groups: [*]const GemvGroup, n_groups: u32) c_int;
+extern fn mmhip_qmm_dev(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?[*]const f32, y_dev: ?[*]f32, batch: u64, out_layout: c_int) c_int;
+extern fn mmhip_qmm_dev_noalloc(ctx: *Ctx, w: *const Weight, mat: u64, x_dev: ?[*]const f32, y_dev: ?[*]f32, batch: u64, out_layout: c_int) c_int;
 extern fn mmhip_moe_layer_create(ctx: *Ctx, wts: *const MoeWeights, out_layer: *?*MoeLayerHandle) c_int;
 extern fn mmhip_moe_layer_destroy(ctx: *Ctx, layer: ?*MoeLayerHandle) void;
 extern fn mmhip_moe_ffn(ctx: *Ctx, layer: *MoeLayerHandle, hidden_host: [*]const f32, out_host: [*]f32, n_tokens: u32, rp: ?*const RouteParams, route_ids_host: ?[*]u32, route_weights_host: ?[*]f32) c_int;
-extern fn mmhip_moe_ffn_dev(ctx: *Ctx, layer: *MoeLayerHandle, hidden_dev: ?*const anyopaque, out_dev: ?*anyopaque, n_tokens: u32, rp: ?*const RouteParams, route_ids_dev: ?*anyopaque, route_weights_dev: ?*anyopaque) c_int;
+extern fn mmhip_moe_ffn_dev(ctx: *Ctx, layer: *MoeLayerHandle, hidden_dev: ?[*]const f32, out_dev: ?[*]f32, n_tokens: u32, rp: ?*const RouteParams, route_ids_dev: ?[*]u32, route_weights_dev: ?[*]f32) c_int;
 extern fn mmhip_moe_expert_counts(ctx: *Ctx, layer: *MoeLayerHandle, counts_host: [*]u64) c_int;
 extern fn mmhip_plan_layer(layer: u32, hp: *const PlanHyperParams, has_gpu: c_int, has_npu: c_int, throttle_level: c_int, db: ?[*]const PerfEntry, db_len: usize, out: [*]OpSchedule, cap: usize, n_out: *usize) c_int;
 extern fn mmhip_plan_critical_path_us(ops: [*]const OpSchedule, n: usize) u64;
@@ -244,18 +256,26 @@ pub const HipBackend = struct {
         return id;
     }
 
-    /// sampleGreedy on device logits (e.g. computeLogits' GEMV output kept
-    /// on the device); the id lands in device memory.
+    /// Several weights' GEMVs (e.g. the routed experts' gate/up and down
+    /// products) in one launch; all weights of one quantised type. No
+    /// reference counterpart: it replaces one matVecMulUnified per matrix
+    /// (inference.zig:1171-1185) with one launch.
+    pub fn gemvGroupedDev(self: *Self, groups: []const GemvGroup) !void {
+        try check(mmhip_gemv_grouped_dev(self.ctx, groups.ptr, @intCast(groups.len)));
+    }
+
     /// The batched QMM on device buffers with the library's fixed scratch:
     /// allocates nothing, for code under graph capture or in loops that must
     /// not allocate. No reference counterpart. batch x cols (rounded up to
     /// 256) x 2.125 bytes must fit the 4,456,448-byte scratch; calls that
     /// overlap on one device race.
-    pub fn qmmDevNoAlloc(self: *Self, w: *const Weight, mat: u64, x_dev: *const anyopaque, y_dev: *anyopaque, batch: u64, out_layout: c_int) !void {
+    pub fn qmmDevNoAlloc(self: *Self, w: *const Weight, mat: u64, x_dev: [*]const f32, y_dev: [*]f32, batch: u64, out_layout: c_int) !void {
         try check(mmhip_qmm_dev_noalloc(self.ctx, w, mat, x_dev, y_dev, batch, out_layout));
     }
 
-    pub fn argmaxDev(self: *Self, out_dev: *anyopaque, logits_dev: *const anyopaque, n: u64) !void {
+    /// sampleGreedy on device logits (e.g. computeLogits' GEMV output kept
+    /// on the device); the id lands in device memory.
+    pub fn argmaxDev(self: *Self, out_dev: *u32, logits_dev: [*]const f32, n: u64) !void {
         try check(mmhip_argmax_dev(self.ctx, out_dev, logits_dev, n));
     }
 
@@ -269,13 +289,13 @@ pub const HipBackend = struct {
 
     /// KVCache.put's Q8_0 branch (kv_cache.zig:289-349) for n_rows device
     /// rows at once (e.g. a prefill's kv_comp rows of kv_lora_rank values).
-    pub fn quantizeRowsQ8_0Dev(self: *Self, blocks_dev: *anyopaque, x_dev: *const anyopaque, x_stride: u64, n_rows: u64, row_len: u32) !void {
+    pub fn quantizeRowsQ8_0Dev(self: *Self, blocks_dev: *anyopaque, x_dev: [*]const f32, x_stride: u64, n_rows: u64, row_len: u32) !void {
         try check(mmhip_quantize_q8_0_rows_dev(self.ctx, blocks_dev, x_dev, x_stride, n_rows, row_len));
     }
 
     /// getKVCompressed / getKPe's Q8_0 branch (kv_cache.zig:225-273) for
     /// n_rows device rows at once.
-    pub fn dequantizeRowsQ8_0Dev(self: *Self, out_dev: *anyopaque, out_stride: u64, blocks_dev: *const anyopaque, n_rows: u64, row_len: u32) !void {
+    pub fn dequantizeRowsQ8_0Dev(self: *Self, out_dev: [*]f32, out_stride: u64, blocks_dev: *const anyopaque, n_rows: u64, row_len: u32) !void {
         try check(mmhip_dequantize_q8_0_rows_dev(self.ctx, out_dev, out_stride, blocks_dev, n_rows, row_len));
     }
 
@@ -329,6 +349,47 @@ pub const MoeLayer = struct {
     /// ExpertStats.counts of this layer.
     pub fn expertCounts(self: *MoeLayer, counts: []u64) !void {
         try check(mmhip_moe_expert_counts(self.backend.ctx, self.handle, counts.ptr));
+    }
+};
+
+// ---- plan dispatch (HeteroExecutor.dispatchGpu, hetero_executor.zig:154-159) ----
+
+/// The GPU side of HeteroExecutor.executeLayer (hetero_executor.zig:88-127)
+/// for the ops planLayer sends to .gpu on a MoE layer (scheduler.zig:473-501
+/// plus this backend's GPU rule): ffn_gate_up, siluMul and ffn_down of the
+/// layer's FFN. The device runs the whole moeFFN (router, Scheduler.route,
+/// expert gate/up, SiLU x up, down, weighted sum and shared expert) in one
+/// call, so ffn_gate_up issues it for the token in `hidden`, siluMul is
+/// already done inside it, and ffn_down hands the result back as moeFFN does
+/// (hidden <- ffn_out, inference.zig:1009; the caller adds the residual).
+/// Ops this backend does not run (attention, RMSNorm, RoPE, or a dense
+/// layer's FFN without a MoeLayer) return error.HipUnsupportedType, and the
+/// executor keeps them on its CPU path.
+pub const PlanDispatch = struct {
+    moe: ?*MoeLayer,
+    /// [hidden_size] buffer owned by the caller: the FFN output between
+    /// ffn_gate_up and ffn_down.
+    ffn_out: []f32,
+    route: RouteParams = .{},
+    pending: bool = false,
+
+    pub fn dispatchGpu(self: *PlanDispatch, op: scheduler.OpSchedule, hidden: []f32) !void {
+        switch (op.op) {
+            .ffn_gate_up => {
+                const L = self.moe orelse return error.HipUnsupportedType;
+                std.debug.assert(hidden.len == L.hidden and self.ffn_out.len == L.hidden);
+                _ = try L.ffn(hidden, self.ffn_out, 1, self.route, null, null);
+                self.pending = true;
+            },
+            // SiLU(gate) * up is formed on the device inside the FFN call.
+            .siluMul => if (!self.pending) return error.HipInvalidArgument,
+            .ffn_down => {
+                if (!self.pending) return error.HipInvalidArgument;
+                @memcpy(hidden, self.ffn_out);
+                self.pending = false;
+            },
+            else => return error.HipUnsupportedType,
+        }
     }
 };
 

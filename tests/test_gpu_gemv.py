@@ -255,3 +255,64 @@ def test_seam_is_thread_safe(ctx, orc):
     for t in th:
         t.join()
     assert len(errs) == 80 and max(errs) <= TOL_GEMV
+
+
+@pytest.mark.parametrize("t", [mm.Q8_0, mm.IQ2_XXS])
+@pytest.mark.parametrize("n_groups", [2, 3, 4])
+def test_gemv_grouped_matches_separate(ctx, orc, t, n_groups):
+    """mmhip_gemv_grouped_dev: weights of different shapes in one launch (the
+    routed experts' gate/up [1536 x 2048] with a shared x, down [2048 x 1536]
+    with one x each, and ragged shapes), against one mmhip_gemv_batched_dev per
+    group (IQ2_XXS: bit for bit; Q8_0: f32 rounding) and the oracle."""
+    rng = np.random.default_rng(700 + 10 * t + n_groups)
+    shapes = [(1536, 2048, 5, True), (2048, 1536, 5, False), (100, 768, 3, False), (48, 2048, 2, True)][:n_groups]
+    groups, sep, cases = [], [], []
+    for rows, cols, n, shared in shapes:
+        raw = mm.make_weight(rng, t, rows, cols, n + 1)
+        w = ctx.upload(raw, t, rows, cols, n + 1)
+        xs = rng.standard_normal((1 if shared else n, cols)).astype(np.float32)
+        dx = mm.DeviceArray.from_numpy(ctx, xs)
+        dy, dy2 = mm.DeviceArray(ctx, n * rows * 4), mm.DeviceArray(ctx, n * rows * 4)
+        groups.append((w, 1, n, dx, 0 if shared else cols, dy, rows))  # matrices 1..n of the stack
+        sep.append((w, dx, dy2, n, 0 if shared else cols, rows))
+        cases.append((raw, xs, rows, cols, n, shared, dy, dy2, w))
+    try:
+        ctx.gemv_grouped_dev(groups)
+        for w, dx, dy2, n, xs_, rows in sep:
+            ctx.gemv_batched_dev(w, 1, n, dx, xs_, dy2, rows)
+        ctx.synchronize()
+        per_mat = mm.tensor_bytes(t, shapes[0][0], shapes[0][1])
+        for raw, xs, rows, cols, n, shared, dy, dy2, w in cases:
+            got = dy.to_numpy(np.float32, n * rows).reshape(n, rows)
+            ref = dy2.to_numpy(np.float32, n * rows).reshape(n, rows)
+            if t == mm.IQ2_XXS:
+                _bits_equal(got, ref)
+            per_mat = mm.tensor_bytes(t, rows, cols)
+            for i in range(n):
+                x = xs[0 if shared else i]
+                cpu = orc.mat_vec_mul_unified(raw[(i + 1) * per_mat:(i + 2) * per_mat], t, x, rows, cols)
+                assert mm.max_abs_rel(got[i], cpu) <= TOL_GEMV
+    finally:
+        for raw, xs, rows, cols, n, shared, dy, dy2, w in cases:
+            dy.free()
+            dy2.free()
+            w.free()
+        for g in groups:
+            g[3].free()
+
+
+def test_gemv_grouped_rejects_bad_groups(ctx):
+    rng = np.random.default_rng(760)
+    wq = ctx.upload(mm.make_weight(rng, mm.Q8_0, 16, 256), mm.Q8_0, 16, 256)
+    wi = ctx.upload(mm.make_weight(rng, mm.IQ2_XXS, 16, 256), mm.IQ2_XXS, 16, 256)
+    x, y = mm.DeviceArray(ctx, 256 * 4), mm.DeviceArray(ctx, 16 * 4)
+    try:
+        with pytest.raises(mm.MmhipError):
+            ctx.gemv_grouped_dev([(wq, 0, 1, x, 0, y, 16), (wi, 0, 1, x, 0, y, 16)])  # two types
+        with pytest.raises(mm.MmhipError):
+            ctx.gemv_grouped_dev([(wq, 0, 2, x, 0, y, 16)])  # past the weight's one matrix
+        with pytest.raises(mm.MmhipError):
+            ctx.gemv_grouped_dev([(wq, 0, 1, x, 0, y, 16)] * 5)  # more than MMHIP_GEMV_MAX_GROUPS
+    finally:
+        for a in (wq, wi, x, y):
+            a.free()
