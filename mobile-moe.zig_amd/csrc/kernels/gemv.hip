@@ -333,8 +333,39 @@ __global__ __launch_bounds__(kFloatThreads) void gemv_strict_kernel(const WT* __
         }
         __syncthreads();
         if (chain) {
+            // The chain's terms in batches of 32 (8 x 16 bytes), read into two
+            // register sets in turn so that the next batch's LDS reads are in
+            // flight while the current one is added (the adds are one
+            // dependent sequence; only the read latency can be hidden). The
+            // read after the last batch re-reads it (clamped) and is unused.
             const float4* pp = reinterpret_cast<const float4*>(&P[tid][0]);
-            for (uint32_t i = 0; i < cn / 16; ++i) {
+            const uint32_t n16 = cn / 16, nb = n16 / 8;
+            float4 ra[8], rb[8];
+            auto read = [&](float4 (&r)[8], uint32_t b) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) r[k] = pp[b * 8 + k];
+                // Keeps the reads issued here, ahead of the adds that follow.
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            auto add = [&](const float4 (&r)[8]) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    acc = acc + r[k].x;
+                    acc = acc + r[k].y;
+                    acc = acc + r[k].z;
+                    acc = acc + r[k].w;
+                }
+            };
+            uint32_t b = 0;
+            if (nb > 0) read(ra, 0);
+            for (; b + 2 <= nb; b += 2) {
+                read(rb, b + 1);
+                add(ra);
+                read(ra, min(b + 2, nb - 1));
+                add(rb);
+            }
+            if (b < nb) add(ra);
+            for (uint32_t i = nb * 8; i < n16; ++i) {
                 const float4 t = pp[i];
                 acc = acc + t.x;
                 acc = acc + t.y;
@@ -342,7 +373,7 @@ __global__ __launch_bounds__(kFloatThreads) void gemv_strict_kernel(const WT* __
                 acc = acc + t.w;
             }
             // cn is a multiple of 4 but not always of 16: the last quad-steps.
-            for (uint32_t i = (cn / 16) * 4; i < cn / 4; ++i) acc = acc + P[tid][i];
+            for (uint32_t i = n16 * 4; i < cn / 4; ++i) acc = acc + P[tid][i];
         }
         __syncthreads();
     }
