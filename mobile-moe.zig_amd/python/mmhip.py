@@ -18,7 +18,9 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.dirname(_HERE)
-LIB_PATH = os.path.join(PKG_DIR, "lib", "libmmhip.so")
+# MMHIP_LIBRARY selects another build of the same library (e.g. the host
+# sanitizer build, lib/libmmhip_san.so).
+LIB_PATH = os.environ.get("MMHIP_LIBRARY") or os.path.join(PKG_DIR, "lib", "libmmhip.so")
 
 F32, F16, Q8_0, IQ2_XXS = 0, 1, 8, 16
 BLOCK_SIZE = {F32: 1, F16: 1, Q8_0: 32, IQ2_XXS: 256}
@@ -182,6 +184,15 @@ class MmhipError(RuntimeError):
         self.code = code
 
 
+def _enc(s: str) -> bytes:
+    """GGUF names and keys are byte strings; non-UTF-8 bytes round-trip."""
+    return s.encode("utf-8", "surrogateescape")
+
+
+def _dec(b: bytes) -> str:
+    return b.decode("utf-8", "surrogateescape")
+
+
 def check(rc: int, what: str) -> int:
     if rc < 0:
         raise MmhipError(what, rc)
@@ -294,7 +305,7 @@ class Context:
         if t is None:
             raise KeyError(name)
         h = _c_void_p()
-        check(self.lib.mmhip_weight_upload_gguf(self.handle, g.handle, name.encode(), ctypes.byref(h)),
+        check(self.lib.mmhip_weight_upload_gguf(self.handle, g.handle, _enc(name), ctypes.byref(h)),
               "mmhip_weight_upload_gguf")
         d = t["dims"]
         return Weight(self, h.value, t["type"], d[1], d[0], d[2])
@@ -304,7 +315,7 @@ class Context:
         ts = [g.tensor(n) for n in names]
         if any(t is None for t in ts):
             raise KeyError([n for n, t in zip(names, ts) if t is None])
-        arr = (ctypes.c_char_p * len(names))(*[n.encode() for n in names])
+        arr = (ctypes.c_char_p * len(names))(*[_enc(n) for n in names])
         h = _c_void_p()
         check(self.lib.mmhip_weight_upload_gguf_rows(self.handle, g.handle, arr, len(names), ctypes.byref(h)),
               "mmhip_weight_upload_gguf_rows")
@@ -446,7 +457,7 @@ class Gguf:
 
     @staticmethod
     def _tensor_dict(t: GgufTensor) -> dict:
-        return dict(name=t.name.decode(), n_dims=t.n_dims, dims=tuple(t.dims), type=t.type, offset=t.offset,
+        return dict(name=_dec(t.name), n_dims=t.n_dims, dims=tuple(t.dims), type=t.type, offset=t.offset,
                     n_elements=t.n_elements, n_bytes=t.n_bytes, data=t.data)
 
     def tensors(self) -> list:
@@ -459,7 +470,7 @@ class Gguf:
 
     def tensor(self, name: str) -> Optional[dict]:
         t = GgufTensor()
-        rc = self.lib.mmhip_gguf_find_tensor(self.handle, name.encode(), ctypes.byref(t))
+        rc = self.lib.mmhip_gguf_find_tensor(self.handle, _enc(name), ctypes.byref(t))
         if rc == self.NOT_FOUND:
             return None
         check(rc, "mmhip_gguf_find_tensor")
@@ -473,25 +484,25 @@ class Gguf:
         return np.ctypeslib.as_array(ctypes.cast(t["data"], ctypes.POINTER(ctypes.c_uint8)), (t["n_bytes"],)).copy()
 
     def keys(self) -> list:
-        return [self.lib.mmhip_gguf_key_at(self.handle, i).decode() for i in range(self.info()["n_keys"])]
+        return [_dec(self.lib.mmhip_gguf_key_at(self.handle, i)) for i in range(self.info()["n_keys"])]
 
     def meta_type(self, key: str) -> Optional[int]:
-        rc = self.lib.mmhip_gguf_meta_type(self.handle, key.encode())
+        rc = self.lib.mmhip_gguf_meta_type(self.handle, _enc(key))
         return None if rc < 0 else rc
 
     def meta_int(self, key: str) -> Optional[int]:
         v = ctypes.c_int64()
-        rc = self.lib.mmhip_gguf_meta_int(self.handle, key.encode(), ctypes.byref(v))
+        rc = self.lib.mmhip_gguf_meta_int(self.handle, _enc(key), ctypes.byref(v))
         return None if rc == self.NOT_FOUND else (check(rc, "mmhip_gguf_meta_int"), v.value)[1]
 
     def meta_float(self, key: str) -> Optional[float]:
         v = ctypes.c_double()
-        rc = self.lib.mmhip_gguf_meta_float(self.handle, key.encode(), ctypes.byref(v))
+        rc = self.lib.mmhip_gguf_meta_float(self.handle, _enc(key), ctypes.byref(v))
         return None if rc == self.NOT_FOUND else (check(rc, "mmhip_gguf_meta_float"), v.value)[1]
 
     def meta_string(self, key: str) -> Optional[bytes]:
         p, n = _c_void_p(), _u64()
-        rc = self.lib.mmhip_gguf_meta_string(self.handle, key.encode(), ctypes.byref(p), ctypes.byref(n))
+        rc = self.lib.mmhip_gguf_meta_string(self.handle, _enc(key), ctypes.byref(p), ctypes.byref(n))
         if rc == self.NOT_FOUND:
             return None
         check(rc, "mmhip_gguf_meta_string")
@@ -500,7 +511,7 @@ class Gguf:
     def meta_array(self, key: str) -> Optional[tuple]:
         """(element type, length, payload bytes)."""
         et, n, p, nb = _u32(), _u64(), _c_void_p(), _u64()
-        rc = self.lib.mmhip_gguf_meta_array(self.handle, key.encode(), ctypes.byref(et), ctypes.byref(n),
+        rc = self.lib.mmhip_gguf_meta_array(self.handle, _enc(key), ctypes.byref(et), ctypes.byref(n),
                                             ctypes.byref(p), ctypes.byref(nb))
         if rc == self.NOT_FOUND:
             return None
