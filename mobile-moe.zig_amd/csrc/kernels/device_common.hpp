@@ -90,6 +90,15 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// A wave-uniform value held in an SGPR from here on. Kernel arguments read
+// through a runtime index (a launch's segment) are otherwise re-loaded where
+// they are used, and each such scalar load inside a loop costs a wait on
+// lgkmcnt, which also waits for the wave's outstanding LDS reads.
+__device__ __forceinline__ uint32_t keep_sgpr(uint32_t v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
 // Waits until all of this wave's vector memory loads have returned
 // (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their no-wait maxima).
 // A CU returns vector loads in issue order across all of its workgroups, so

@@ -124,6 +124,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
     const BufRsrc d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
     const uint32_t rec_voff = lane * 16;
     const uint32_t d_voff = n * a.d_row * 2;
+    const uint32_t rec_tile = keep_sgpr(a.units * 1024u), d_tile = keep_sgpr(a.d_row * 32u);
 
     // Per-chunk split (set by start_chunk).
     uint32_t u_begin = 0, S = 1, L = 0, j0 = 0, j1 = 0, tf = 0;
@@ -141,8 +142,8 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
         uint32_t rs = kBufOob, ds = kBufOob;
         if (valid) {
             const uint32_t t = t_begin + q.t, u = u_begin + q.s * UPS;
-            rs = (t * a.units + u) * 1024;
-            ds = (t * 16 * a.d_row + u * 2) * 2;
+            rs = t * rec_tile + u * 1024;
+            ds = t * d_tile + u * 4;
         }
         load_step<FMT, UPS>(rec_r, rec_voff, rs, d_r, d_voff, ds, r, dw);
     };

@@ -218,6 +218,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     BufRsrc rec_r, d_r;
     const uint32_t rec_voff = lane * 16;
     const uint32_t d_voff = n * a.d_row * 2;
+    const uint32_t rec_tile = keep_sgpr(a.units * 1024u), d_tile = keep_sgpr(a.d_row * 32u);
     // Sparse A row of this lane: block s_star of the unit, digit d_star.
     const uint32_t s_star = (n >> 2) + 4 * ((n >> 1) & 1u), d_star = n & 1u;
 
@@ -242,8 +243,8 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
             const uint32_t tl = 2 * q.t + h;
             if (valid && tl < n_tiles) {
                 const uint32_t tile = t_begin + tl, u = u0 + q.ul;
-                rs = (tile * a.units + u) * 1024;
-                ds = (tile * 16 * a.d_row + u) * 2;
+                rs = tile * rec_tile + u * 1024;
+                ds = tile * d_tile + u * 2;
             }
             r[h] = buf_load_b128<kCacheStream>(rec_r, rec_voff, rs);
             dbits[h] = buf_load_b16(d_r, d_voff, ds);  // cached: the tile's other units reuse the line
