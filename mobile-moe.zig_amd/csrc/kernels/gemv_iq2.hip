@@ -417,6 +417,205 @@ static uint32_t max_tiles_per_wg(const GemvArgs& a) {
     return a.tiles < m ? a.tiles : m;
 }
 
+// Decode down projection and combine of one token (IQ2_XXS experts): the
+// down GEMVs of every computed expert (up to kMaxK routed + the merged
+// shared expert) and moeFFN's final sum (inference.zig:960-1010) in one
+// launch. Workgroup t owns row tile t of every problem, so the weighted sum
+// over the experts needs no other workgroup: all problems' weight loads and
+// activation loads are issued up front, the activations silu(g) * u are
+// quantised into LDS side by side (unit u' = p * units + u), each wave takes
+// items (p, u) with the decode GEMV's arithmetic, and the tile's 16 rows are
+// then summed per problem (units in order, lane groups in order, as the
+// decode GEMV does) and combined in route order as combine_kernel does.
+constexpr int kDcWg = 1024;
+constexpr uint32_t kDcWaves = kDcWg / 64;
+constexpr uint32_t kDcMaxProbs = kMaxK + 1;
+constexpr uint32_t kDcMaxUnits = 8;  // inner width <= 2048
+constexpr uint32_t kDcMaxItems = kDcMaxProbs * kDcMaxUnits;
+constexpr uint32_t kDcItemsPerWave = (kDcMaxItems + kDcWaves - 1) / kDcWaves;
+
+// silu(x) = x / (1 + e^-x) (math.zig:38-41) with the hardware exp2 and
+// reciprocal (a few ulp from the correctly rounded quotient): each workgroup
+// here forms every expert's activation, so the IEEE division and expf would
+// dominate its arithmetic.
+__device__ __forceinline__ float silu_fast(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
+__global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineArgs a) {
+    struct Lds {
+        uint32_t tab[kIq2TableWords];
+        uint32_t mtab[8];
+        uint8_t aq[kDcMaxItems * 8 * 64];
+        float xs[kDcMaxItems * 8];
+        float part[kDcMaxItems * 64];
+        float ysum[kDcMaxProbs * 16];
+        float cw[kMaxK];        // route weights of the computed entries
+        int32_t cs[kMaxK + 1];  // their slots, then the shared slot (-1: none)
+    };
+    __shared__ __align__(16) Lds lds;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t n = lane & 15, g = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tile = blockIdx.x;
+    const uint32_t units = a.units, nblk = units * 8;
+    // The count and the whole problem list in one round trip (the list
+    // always has kDcMaxProbs entries; those past the count are ignored).
+    uint4 prob[kDcMaxProbs];
+#pragma unroll
+    for (uint32_t p = 0; p < kDcMaxProbs; ++p) prob[p] = a.probs[p];
+    const uint32_t n_act = min(*a.n_active, kDcMaxProbs);
+    const uint32_t n_items = n_act * units;
+    uint32_t slot[kDcMaxProbs];
+#pragma unroll
+    for (uint32_t p = 0; p < kDcMaxProbs; ++p) {
+        if (p >= n_act) prob[p] = make_uint4(0, 0, 0xFFFFFFFFu, 0);
+        slot[p] = prob[p].z;
+    }
+
+    // Small loads first: tables, every problem's activation pair.
+    constexpr int kTabPer = kIq2TableWords / 4 / kDcWg;
+    const BufRsrc t_r = make_rsrc(&c_iq2_tables, sizeof(Iq2Tables));
+    uint4 tv[kTabPer];
+#pragma unroll
+    for (int i = 0; i < kTabPer; ++i) tv[i] = buf_load_b128(t_r, (threadIdx.x + kDcWg * i) * 16, 0);
+    // The combine's inputs, read now so their latency overlaps the loads.
+    const uint32_t row = tile * 16 + (threadIdx.x & 15);
+    const float bias_v = (a.bias && threadIdx.x < 16 && row < a.rows) ? a.bias[row] : 0.0f;
+    const uint32_t deferred = a.deferred[0];
+    float cw = 0.0f;
+    int32_t cs = -1;
+    if (threadIdx.x < kMaxK) {
+        cs = a.assign_slot[threadIdx.x];
+        cw = a.assign_w[threadIdx.x];
+    } else if (threadIdx.x == kMaxK) {
+        cs = a.shared_slot[0];
+    }
+    // The problems' blocks side by side: global block B = p * nblk + b, 8
+    // lanes (4 columns each) per block, kDcWg / 8 blocks per pass.
+    constexpr uint32_t kPassBlocks = kDcWg / 8;
+    constexpr uint32_t kPasses = (kDcMaxItems * 8 + kPassBlocks - 1) / kPassBlocks;
+    const uint32_t xbytes = (uint32_t)((kDcMaxProbs * a.x_stride) * 4);
+    const BufRsrc xr = make_rsrc(a.x, xbytes);
+    float xv[kPasses][4], uv[kPasses][4];
+#pragma unroll
+    for (uint32_t q = 0; q < kPasses; ++q) {
+        const uint32_t B = q * kPassBlocks + (threadIdx.x >> 3);
+        const uint32_t p = B / nblk, c = (B - p * nblk) * 32 + 4 * (threadIdx.x & 7);
+        uint32_t xrow = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < kDcMaxProbs; ++r)
+            if (r == p) xrow = prob[r].y;
+        const bool ok = p < n_act && c < a.cols;
+        const uint32_t o0 = ok ? (uint32_t)((xrow * a.x_stride + c) * 4) : kBufOob;
+        const uint32_t o1 = ok ? (uint32_t)((xrow * a.x_stride + a.x2_off + c) * 4) : kBufOob;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            xv[q][e] = __uint_as_float(buf_load_b32(xr, o0 + 4 * e, 0));
+            uv[q][e] = __uint_as_float(buf_load_b32(xr, o1 + 4 * e, 0));
+        }
+    }
+    // Every wave's small loads are issued before any weight load: a CU
+    // returns loads in issue order.
+    __builtin_amdgcn_s_barrier();
+    // Weight items of this wave: item i = p * units + u, i = wave + kDcWaves j.
+    uint4 rb[kDcItemsPerWave];
+    uint32_t db[kDcItemsPerWave];
+    const uint32_t rec_voff = lane * 16, d_voff = n * a.d_row * 2;
+#pragma unroll
+    for (uint32_t j = 0; j < kDcItemsPerWave; ++j) {
+        const uint32_t i = wave + kDcWaves * j;
+        const bool ok = i < n_items;
+        const uint32_t p = ok ? i / units : 0, u = i - p * units;
+        uint64_t mat = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < kDcMaxProbs; ++q)
+            if (ok && q == p) mat = prob[q].x;
+        const BufRsrc rr = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
+        const BufRsrc dr = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
+        rb[j] = buf_load_b128<kCacheStream>(rr, rec_voff, ok ? (tile * units + u) * 1024 : kBufOob);
+        db[j] = buf_load_b16(dr, d_voff, ok ? (tile * 16 * a.d_row + u) * 2 : kBufOob);
+    }
+#pragma unroll
+    for (int i = 0; i < kTabPer; ++i) reinterpret_cast<uint4*>(lds.tab)[threadIdx.x + kDcWg * i] = tv[i];
+    if (threadIdx.x < 8) lds.mtab[threadIdx.x] = nibble_byte_mask(threadIdx.x | (parity3(threadIdx.x) << 3));
+    if (threadIdx.x <= kMaxK) {
+        lds.cs[threadIdx.x] = cs;
+        if (threadIdx.x < kMaxK) lds.cw[threadIdx.x] = cw;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kPasses; ++q) {
+        if (q * kPassBlocks >= n_items * 8) break;  // uniform
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[q][e] = silu_fast(xv[q][e]) * uv[q][e];
+        // Every thread quantises (the block max uses DPP); blocks of
+        // problems that run are stored.
+        x_store_planes(xv[q], n_items * 8, q * kPassBlocks, lds.aq, lds.xs);
+    }
+    lds_barrier();
+
+    const uint32_t s_star = (n >> 2) + 4 * ((n >> 1) & 1u), d_star = n & 1u;
+#pragma unroll
+    for (uint32_t j = 0; j < kDcItemsPerWave; ++j) {
+        const uint32_t i = wave + kDcWaves * j;
+        if (i >= n_items) break;
+        RawB raw;
+        fetch_b(rb[j], lds.tab, lds.mtab, raw);
+        const uint2 xw = *reinterpret_cast<const uint2*>(lds.aq + ((i * 8 + s_star) * 2 + d_star) * 32 + 8 * g);
+        v4i av[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool lo = s_star == 2u * q, hi = s_star == 2u * q + 1;
+            av[q] = v4i{(int)(lo ? xw.x : 0u), (int)(lo ? xw.y : 0u), (int)(hi ? xw.x : 0u), (int)(hi ? xw.y : 0u)};
+        }
+        const float xa = lds.xs[i * 8 + g] * 0.25f, xb4 = lds.xs[i * 8 + g + 4] * 0.25f;
+        long b[8];
+        finish_b(raw, b);
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], bpair(b, q), acc, 0, 0, 0);
+        const float sa = fmaf((float)iq2_ls_a(rb[j]), xa, xa * 0.5f);
+        const float sb = fmaf((float)iq2_ls_b(rb[j]), xb4, xb4 * 0.5f);
+        float v = (float)digits_combine(acc[0], acc[1]) * sa;
+        v = fmaf((float)digits_combine(acc[2], acc[3]), sb, v);
+        lds.part[i * 64 + lane] = v * f16_scale(db[j]);
+    }
+    lds_barrier();
+    if (threadIdx.x < 16 * kDcMaxProbs) {
+        // Row r of problem p: the decode GEMV's row sum (units, then lane
+        // groups, in order, added to a zero row).
+        const uint32_t p = threadIdx.x >> 4, r = threadIdx.x & 15;
+        if (p < n_act) {
+            float sum = 0.0f;
+            for (uint32_t u = 0; u < units; ++u) {
+                const float* pp = lds.part + (p * units + u) * 64 + r;
+                sum += ((pp[0] + pp[16]) + pp[32]) + pp[48];
+            }
+            lds.ysum[p * 16 + r] = 0.0f + sum;
+        }
+    }
+    lds_barrier();
+    if (threadIdx.x < 16 && row < a.rows) {
+        // Slot s (route order, shared last) -> its problem's row value.
+        auto slot_val = [&](int32_t s) {
+            float v = 0.0f;
+            for (uint32_t p = 0; p < n_act; ++p)
+                if (slot[p] == (uint32_t)s) v = lds.ysum[p * 16 + threadIdx.x];
+            return v;
+        };
+        float o = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxK; ++i) {
+            const int32_t sl = lds.cs[i];
+            if (sl >= 0) o = __fadd_rn(o, __fmul_rn(lds.cw[i], slot_val(sl)));
+        }
+        const int32_t sh = lds.cs[kMaxK];
+        if (sh >= 0) o = __fadd_rn(o, slot_val(sh));
+        if (a.bias && deferred) o = __fadd_rn(o, bias_v);
+        a.out[row] = o;
+    }
+}
+
 template <int N>
 static hipError_t launch_set(const GemvArgs* segs, uint32_t n_segs, const void* fn, uint32_t grid_x, hipStream_t s) {
     GemvSet<N> set{};
@@ -499,6 +698,16 @@ hipError_t launch_gemv_iq2(const GemvArgs* segs_in, uint32_t n_segs, int num_cu,
     if (n == 2)
         return launch_set<2>(segs, 2, reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 2>), grid_x, s);
     return launch_set<4>(segs, n, reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 4>), grid_x, s);
+}
+
+hipError_t launch_down_combine_iq2(const DownCombineArgs& a, hipStream_t s) {
+    if (a.units == 0 || a.units > kDcMaxUnits || a.tiles == 0 || a.cols > a.units * 256 ||
+        a.x2_off + a.cols > a.x_stride || (uint64_t)kDcMaxProbs * a.x_stride * 4 >= (1ull << 31))
+        return hipErrorInvalidValue;
+    DownCombineArgs args = a;
+    void* kargs[] = {&args};
+    return hipLaunchKernel(reinterpret_cast<const void*>(&down_combine_iq2_kernel), dim3(a.tiles), dim3(kDcWg), kargs,
+                           0, s);
 }
 
 }  // namespace mmhip

@@ -145,6 +145,30 @@ hipError_t launch_gemv_segments(const GemvArgs* segs, uint32_t n_segs, uint32_t 
 // forward IQ2_XXS here.
 hipError_t launch_gemv_iq2(const GemvArgs* segs, uint32_t n_segs, int num_cu, hipStream_t s);
 
+// Decode (one token) down projection of the computed experts and the
+// combine, IQ2_XXS experts with the shared expert merged (or none): problem
+// p of probs[0, *n_active) is {matrix, activation slot, output slot, 0};
+// its input is silu(x[slot]) * x[slot] + x2_off (rows x_stride floats
+// apart). out = the combined token (combine_kernel's sum).
+struct DownCombineArgs {
+    const uint4* recs;
+    const uint16_t* dvals;
+    uint64_t rec_stride, d_stride;
+    uint32_t d_row;
+    const uint4* probs;
+    const uint32_t* n_active;
+    const float* x;
+    uint64_t x_stride, x2_off;
+    const int32_t* assign_slot;
+    const float* assign_w;
+    const int32_t* shared_slot;
+    const uint32_t* deferred;
+    const float* bias;              // or null
+    float* out;
+    uint32_t tiles, units, rows, cols;
+};
+hipError_t launch_down_combine_iq2(const DownCombineArgs& a, hipStream_t s);
+
 // Allocation-free QMM scratch (noalloc.hip): kNoallocScratchBytes of device
 // memory per device, kept until the process ends. noalloc_scratch() returns
 // this device's address; call it with `device` current. Every call on a

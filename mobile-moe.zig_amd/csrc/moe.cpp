@@ -12,7 +12,9 @@
 //                   workgroup routes the token itself and one
 //                   writes the routing outputs               "moe_gateup"
 //     down          quantised GEMV, input silu(gate) * up
-//                   formed while quantising                  "moe_down"
+//                   formed while quantising; with IQ2_XXS
+//                   experts (shared merged) it also does the
+//                   combine in the same launch               "moe_down"
 //   T > 1 (prefill, experts grouped):
 //     quantise hidden (with IQ2_XXS experts: inside the
 //     routing launch)                                         "moe_quantize"
@@ -243,6 +245,33 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
                             L->y_gu, I, &r));
         if (sep_shared)
             MOE_TRY(gemv_launch(ctx, L->sh_gu, "moe_gateup", nullptr, nullptr, 2, hidden, 0, 0, false, L->y_sh, SI));
+        const TileGeom& gd = L->dn->geom;
+        if (!sep_shared && gd.fmt == kFmtIq2 && gd.units <= 8) {
+            // Down projection and combine in one launch.
+            DownCombineArgs d{};
+            d.recs = L->dn->recs;
+            d.dvals = L->dn->dvals;
+            d.rec_stride = gd.rec_stride;
+            d.d_stride = gd.d_stride;
+            d.d_row = (uint32_t)gd.d_row;
+            d.probs = L->gemv_dn;
+            d.n_active = L->n_gemv + 1;
+            d.x = L->y_gu;
+            d.x_stride = 2 * (uint64_t)I;
+            d.x2_off = I;
+            d.assign_slot = L->assign_slot;
+            d.assign_w = L->assign_w;
+            d.shared_slot = L->shared_slot;
+            d.deferred = L->deferred;
+            d.bias = with_bias ? L->bias : nullptr;
+            d.out = out;
+            d.tiles = (uint32_t)gd.tiles;
+            d.units = (uint32_t)gd.units;
+            d.rows = (uint32_t)gd.rows;
+            d.cols = (uint32_t)gd.cols;
+            TimedLaunch tl(ctx, "moe_down");
+            return check_hip(launch_down_combine_iq2(d, s), "moe: down + combine");
+        }
         MOE_TRY(gemv_launch(ctx, L->dn, "moe_down", L->gemv_dn, L->n_gemv + 1, 5, L->y_gu, 2 * (uint64_t)I, I, true,
                             L->eo, H));
         if (sep_shared)
