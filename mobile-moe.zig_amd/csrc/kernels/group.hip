@@ -333,18 +333,15 @@ int env_int(const char* name, int dflt) {
     return e ? atoi(e) : dflt;
 }
 
-// Units per step: the largest of 4, 3, 2, 1 (IQ2_XXS: of 2, 1) dividing both
-// the tile's units and a chunk's (Q8_0 tiles hold a multiple of 4 units).
-// Measured on MI355X (batch 64): IQ2_XXS steps of two units with 512-thread
-// workgroups hold fewer registers and run four waves per SIMD, 7% faster
-// than four-unit steps with 256 threads; Q8_0 is fastest with the latter.
-// Overrides: MMHIP_GROUP_UPS (1..4), MMHIP_GROUP_WG (256 | 512).
-int group_ups(uint32_t fmt, uint32_t units) {
+// Units per step: the largest of 4, 3, 2, 1 (with `most` below 4: of most
+// and below) dividing both the tile's units and a chunk's (Q8_0 tiles hold a
+// multiple of 4 units). Override: MMHIP_GROUP_UPS (1..4).
+int group_ups(uint32_t units, uint32_t fmt, int most) {
     const uint32_t per_chunk = kGChunkBlocks / (fmt == kFmtIq2 ? 8 : 2);
     const uint32_t cu = units < per_chunk ? units : per_chunk;
     static const int most_env = env_int("MMHIP_GROUP_UPS", 0);
-    const int most = most_env >= 1 && most_env <= 4 ? most_env : (fmt == kFmtIq2 ? 2 : 4);
-    for (int u = most; u >= 1; --u)
+    if (most_env >= 1 && most_env <= 4) most = most_env;
+    for (int u = most < 1 || most > 4 ? 4 : most; u >= 1; --u)
         if (units % u == 0 && cu % u == 0) return u;
     return 1;
 }
@@ -363,9 +360,18 @@ int resident(const void* fn, int wg) {
 
 hipError_t launch(GroupArgs a, uint32_t fmt, uint32_t items, int num_cu, hipStream_t s) {
     if (items == 0 || a.tiles == 0) return hipSuccess;
+    // Workgroup size and step: measured on MI355X at batch 64, IQ2_XXS
+    // grouped experts run 7% faster with 512 threads and two-unit steps
+    // (fewer registers: four waves per SIMD) than with 256 threads and
+    // four-unit steps, when the call has at least one 512-thread workgroup's
+    // tiles per CU; smaller calls (an MLA projection at 64 tokens) would
+    // leave CUs idle and keep 256 threads. Q8_0 is fastest with 256 / 4.
+    // Override: MMHIP_GROUP_WG (256 | 512).
     static const int wg_env = env_int("MMHIP_GROUP_WG", 0);
-    const int wg = wg_env == 512 || wg_env == 256 ? wg_env : (fmt == kFmtIq2 ? 512 : 256);
-    const int ups = group_ups(fmt, a.units);
+    const uint64_t cus = (uint64_t)(num_cu > 0 ? num_cu : 256);
+    const bool wide = fmt == kFmtIq2 && (uint64_t)items * a.tiles >= cus * 8;
+    const int wg = wg_env == 512 || wg_env == 256 ? wg_env : (wide ? 512 : 256);
+    const int ups = group_ups(a.units, fmt, wg == 512 ? 2 : 4);
     const void* fn = fmt == kFmtIq2 ? (wg == 512 ? group_kernel_for<kFmtIq2, 512>(ups) : group_kernel_for<kFmtIq2, 256>(ups))
                                     : (wg == 512 ? group_kernel_for<kFmtQ8, 512>(ups) : group_kernel_for<kFmtQ8, 256>(ups));
     // Every resident workgroup slot of the device, or fewer when the largest
@@ -373,7 +379,7 @@ hipError_t launch(GroupArgs a, uint32_t fmt, uint32_t items, int num_cu, hipStre
     // workgroup takes 1 / grid of the items' tiles (the actual item count
     // of a grouped call is only known on the device).
     const uint32_t waves = wg / 64;
-    const uint64_t slots = (uint64_t)(num_cu > 0 ? num_cu : 256) * resident(fn, wg);
+    const uint64_t slots = cus * resident(fn, wg);
     const uint64_t most = ((uint64_t)items * a.tiles + waves - 1) / waves;
     const dim3 grid((unsigned)(most < slots ? most : slots));
     void* args[] = {&a};
