@@ -29,7 +29,8 @@
 //   (d >> 15) & 0x7FF8 for 2k+1), holds all eight weights with the signs of
 //   b012, P (column 3: P ^ parity(b012)) and column 7 = P; the hi3 signs
 //   (columns 4..6, and column 7 flipped by parity(hi3): the ksigns parity
-//   bit) are applied in registers (iq2_fix_hi).
+//   bit) come from an 8-entry table of byte masks right after it, keyed by
+//   hi3, and are applied with one xor-add (negate_bytes).
 //
 //   Q8_0 unit (two 32-column blocks of 16 rows, 1088 B = 32 x 34 B):
 //     recs: lane l holds qs[8g..8g+7] of block 2u then of block 2u+1.
@@ -55,6 +56,8 @@ constexpr int kIq2UnitCols = 256;
 constexpr int kQ8UnitCols = 64;
 constexpr float kDigitMax = 32512.0f;  // 127 * 256: hi digit stays in [-127, 127]
 constexpr int kIq2TableWords = 8192;   // 4096 record entries of two u32
+constexpr int kIq2MaskWords = 8;       // hi3 sign masks, after the record entries in LDS
+constexpr int kIq2LdsWords = kIq2TableWords + kIq2MaskWords;
 // LDS A layout (decode): per 256-column group, lane (m = 0|1, g) owns a
 // 64-byte run holding the 8 A operands (8 x 8 digits) of the group's 8
 // blocks for A row m (hi/lo digits) and column group g; runs are 80 B apart so
@@ -170,39 +173,27 @@ __host__ __device__ constexpr uint32_t negate_bytes(uint32_t w, uint32_t mask) {
     return (w ^ mask) + (mask & 0x01010101u);
 }
 
-// Byte masks for the hi3 signs of a record: for hi3 = h, bit 15 - h of
-// kIq2FixS1 is hi3 bit 0 and bit 31 - h hi3 bit 1; bits 15 - h / 31 - h of
-// kIq2FixS0 are hi3 bit 2 and parity(hi3). Shifted left by h, these bits sit
-// at 15 and 31, where v_perm_b32's sign-replicating selectors (8: bit 15 of
-// the second operand, 9: its bit 31, 10/11: bits 15/31 of the first) turn
-// them into 0x00 / 0xFF bytes.
-__host__ __device__ constexpr uint32_t iq2_fix_const(bool high) {
-    uint32_t c = 0;
-    for (uint32_t h = 0; h < 8; ++h) {
-        const uint32_t a = high ? (h >> 2) & 1u : h & 1u;
-        const uint32_t b = high ? parity3(h) : (h >> 1) & 1u;
-        c |= a << (15 - h);
-        c |= b << (31 - h);
-    }
-    return c;
-}
-constexpr uint32_t kIq2FixS1 = iq2_fix_const(false);
-constexpr uint32_t kIq2FixS0 = iq2_fix_const(true);
+// Byte mask (0xFF per byte to negate) of columns 4..7 for hi3 = h: columns
+// 4..6 take h's bits, column 7 its parity (the ksigns parity bit; column 7's
+// P sign is already in the record entry).
+__host__ __device__ constexpr uint32_t iq2_hi3_mask(uint32_t h) { return nibble_byte_mask(h | (parity3(h) << 3)); }
 
-// Columns 4..7 of a record from the table's word (signs for hi3 = 0) and hi3.
-__device__ __forceinline__ uint32_t iq2_fix_hi(uint32_t w, uint32_t hi3) {
-    const uint32_t m = __builtin_amdgcn_perm(kIq2FixS0 << hi3, kIq2FixS1 << hi3, 0x0B0A0908u);
-    return negate_bytes(w, m);
+// IQ2_XXS B operands of the two records in one tile dword, from the LDS
+// record entries and hi3 masks (tab: kIq2LdsWords words). The mask reads
+// touch at most 8 words: broadcasts without bank conflicts.
+__device__ __forceinline__ long iq2_bop(uint32_t entry_off, uint32_t mask_off, const uint32_t* __restrict__ tab) {
+    const char* t8 = reinterpret_cast<const char*>(tab);
+    const uint2 e = *reinterpret_cast<const uint2*>(t8 + entry_off);
+    const uint32_t m = *reinterpret_cast<const uint32_t*>(t8 + kIq2TableWords * 4 + mask_off);
+    return (long)(((uint64_t)negate_bytes(e.y, m) << 32) | (uint64_t)e.x);
 }
-
-// IQ2_XXS B operands of the two records in one tile dword.
+// Sub-block 2k: entry at bits 3..14, hi3 at bits 15..17.
 __device__ __forceinline__ long iq2_bop_lo(uint32_t d, const uint32_t* __restrict__ tab) {
-    const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(tab) + (d & 0x7FF8u));
-    return (long)(((uint64_t)iq2_fix_hi(e.y, (d >> 15) & 7u) << 32) | (uint64_t)e.x);
+    return iq2_bop(d & 0x7FF8u, (d >> 13) & 0x1Cu, tab);
 }
+// Sub-block 2k + 1: entry at bits 18..29, hi3 at bits 0..2.
 __device__ __forceinline__ long iq2_bop_hi(uint32_t d, const uint32_t* __restrict__ tab) {
-    const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(tab) + ((d >> 15) & 0x7FF8u));
-    return (long)(((uint64_t)iq2_fix_hi(e.y, d & 7u) << 32) | (uint64_t)e.x);
+    return iq2_bop((d >> 15) & 0x7FF8u, (d << 2) & 0x1Cu, tab);
 }
 
 // ls of sub-block g (from dwords 0,1) and 4+g (dwords 2,3) of this lane.
@@ -265,9 +256,11 @@ struct Iq2TableCopy {
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) v[i] = buf_load_b128(r, (threadIdx.x + WG * i) * 16, 0);
     }
+    // tab: kIq2LdsWords words (record entries, then the hi3 masks).
     __device__ __forceinline__ void store(uint32_t* tab) const {
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) reinterpret_cast<uint4*>(tab)[threadIdx.x + WG * i] = v[i];
+        if (threadIdx.x < kIq2MaskWords) tab[kIq2TableWords + threadIdx.x] = iq2_hi3_mask(threadIdx.x);
     }
 };
 

@@ -308,7 +308,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
         if (threadIdx.x < 8) {
             // Columns 4..6 take hi3's bits, column 7 its parity (the ksigns
             // parity bit; column 7's P sign is already in the table word).
-            lds.mtab[threadIdx.x] = nibble_byte_mask(threadIdx.x | (parity3(threadIdx.x) << 3));
+            lds.mtab[threadIdx.x] = iq2_hi3_mask(threadIdx.x);
         }
         for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += kQWg) row_sum[i] = 0.0f;
         if (silu_mul) silu_mul4(xv, uv);
@@ -538,7 +538,7 @@ __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineA
     }
 #pragma unroll
     for (int i = 0; i < kTabPer; ++i) reinterpret_cast<uint4*>(lds.tab)[threadIdx.x + kDcWg * i] = tv[i];
-    if (threadIdx.x < 8) lds.mtab[threadIdx.x] = nibble_byte_mask(threadIdx.x | (parity3(threadIdx.x) << 3));
+    if (threadIdx.x < 8) lds.mtab[threadIdx.x] = iq2_hi3_mask(threadIdx.x);
     if (threadIdx.x <= kMaxK) {
         lds.cs[threadIdx.x] = cs;
         if (threadIdx.x < kMaxK) lds.cw[threadIdx.x] = cw;

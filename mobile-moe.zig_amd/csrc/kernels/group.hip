@@ -126,11 +126,14 @@ __device__ __forceinline__ void step_group_q8(const uint4 (&r)[kMaxUnitsPerStep]
     }
 }
 
+// The launch bound's second argument is the minimum waves per SIMD: two
+// 512-thread IQ2_XXS workgroups share a CU (their LDS fits twice), four waves
+// per SIMD, so at most 128 registers.
 template <int FMT, int UPS, int WG>
-__global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArgs a) {
+__global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG == 512) ? 4 : 2) void group_kernel(GroupArgs a) {
     constexpr uint32_t kWaves = WG / 64;
     constexpr uint32_t kBlkPerUnit = (FMT == kFmtIq2) ? 8 : 2;
-    __shared__ __align__(16) uint32_t tab[FMT == kFmtIq2 ? kIq2TableWords : 4];
+    __shared__ __align__(16) uint32_t tab[FMT == kFmtIq2 ? kIq2LdsWords : 4];
     __shared__ __align__(16) uint8_t aq[kGChunkBlocks * 512];
     __shared__ __align__(16) float xs_lds[kGRows * kGChunkBlocks];
 
@@ -212,7 +215,9 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
     // Stage chunk [kb, kb + nb) of the item's activations: thread t moves the
     // 16-byte A words c = t + i * WG and the scales (j, b) = t + i * WG.
     constexpr uint32_t kPer = kGStage / WG;
-    auto stage_load = [&](uint32_t kb0, uint32_t nb, uint2 (&lo)[kPer], uint2 (&hi)[kPer], float (&sc)[2]) {
+    constexpr uint32_t kScales = kGRows * kGChunkBlocks;
+    constexpr uint32_t kPerSc = (kScales + WG - 1) / WG;
+    auto stage_load = [&](uint32_t kb0, uint32_t nb, uint2 (&lo)[kPer], uint2 (&hi)[kPer], float (&sc)[kPerSc]) {
 #pragma unroll
         for (uint32_t i = 0; i < kPer; ++i) {
             const uint32_t c = threadIdx.x + i * WG;
@@ -224,22 +229,22 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
             hi[i] = *reinterpret_cast<const uint2*>(src + 32);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t e = threadIdx.x + i * WG;  // < 512 = kGRows * kGChunkBlocks
-            const uint32_t j = e / kGChunkBlocks, b = e % kGChunkBlocks;
+        for (uint32_t i = 0; i < kPerSc; ++i) {
+            const uint32_t e = threadIdx.x + i * WG;
+            const uint32_t j = (e < kScales ? e : 0) / kGChunkBlocks, b = e % kGChunkBlocks;
             sc[i] = a.xs[act_row(j) * a.xs_stride + kb0 + (b < nb ? b : 0)];
         }
     };
-    auto stage_store = [&](uint32_t nb, const uint2 (&lo)[kPer], const uint2 (&hi)[kPer], const float (&sc)[2]) {
+    auto stage_store = [&](uint32_t nb, const uint2 (&lo)[kPer], const uint2 (&hi)[kPer], const float (&sc)[kPerSc]) {
 #pragma unroll
         for (uint32_t i = 0; i < kPer; ++i) {
             const uint32_t c = threadIdx.x + i * WG;
             if (2 * (c >> 6) < nb) *reinterpret_cast<uint4*>(aq + c * 16) = make_uint4(lo[i].x, lo[i].y, hi[i].x, hi[i].y);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (uint32_t i = 0; i < kPerSc; ++i) {
             const uint32_t e = threadIdx.x + i * WG;
-            if (e % kGChunkBlocks < nb) xs_lds[e] = sc[i];
+            if (e < kScales && e % kGChunkBlocks < nb) xs_lds[e] = sc[i];
         }
     };
 
@@ -274,7 +279,7 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
         Iq2TableCopy<WG> tc;
         if (FMT == kFmtIq2) tc.load();
         uint2 lo[kPer], hi[kPer];
-        float sc[2];
+        float sc[kPerSc];
         stage_load(0, chunk_blk, lo, hi, sc);
         vm_wait_all();
         if (FMT == kFmtIq2) tc.store(tab);
@@ -308,7 +313,7 @@ __global__ __launch_bounds__(WG, (WG == 256 ? 2 : 1)) void group_kernel(GroupArg
         }
         lds_barrier();  // the previous chunk's LDS no longer in use
         uint2 lo[kPer], hi[kPer];
-        float sc[2];
+        float sc[kPerSc];
         stage_load(kb0, nb, lo, hi, sc);
         if (kb0 == 0) vm_wait_all();  // a new item: small loads ahead of its weights
         load(0, r0, d0);
@@ -361,17 +366,18 @@ int resident(const void* fn, int wg) {
 hipError_t launch(GroupArgs a, uint32_t fmt, uint32_t items, int num_cu, hipStream_t s) {
     if (items == 0 || a.tiles == 0) return hipSuccess;
     // Workgroup size and step: measured on MI355X at batch 64, IQ2_XXS
-    // grouped experts run 7% faster with 512 threads and two-unit steps
-    // (fewer registers: four waves per SIMD) than with 256 threads and
-    // four-unit steps, when the call has at least one 512-thread workgroup's
-    // tiles per CU; smaller calls (an MLA projection at 64 tokens) would
-    // leave CUs idle and keep 256 threads. Q8_0 is fastest with 256 / 4.
+    // grouped experts run ~10% faster with 512 threads and one-unit steps
+    // (98 registers: four waves per SIMD; two-unit steps need 128 and
+    // spill) than with 256 threads and four-unit steps, when the call has at
+    // least one 512-thread workgroup's tiles per CU; smaller calls (an MLA
+    // projection at 64 tokens) would leave CUs idle and keep 256 threads.
+    // Q8_0 is fastest with 256 / 4.
     // Override: MMHIP_GROUP_WG (256 | 512).
     static const int wg_env = env_int("MMHIP_GROUP_WG", 0);
     const uint64_t cus = (uint64_t)(num_cu > 0 ? num_cu : 256);
     const bool wide = fmt == kFmtIq2 && (uint64_t)items * a.tiles >= cus * 8;
     const int wg = wg_env == 512 || wg_env == 256 ? wg_env : (wide ? 512 : 256);
-    const int ups = group_ups(a.units, fmt, wg == 512 ? 2 : 4);
+    const int ups = group_ups(a.units, fmt, wg == 512 ? 1 : 4);
     const void* fn = fmt == kFmtIq2 ? (wg == 512 ? group_kernel_for<kFmtIq2, 512>(ups) : group_kernel_for<kFmtIq2, 256>(ups))
                                     : (wg == 512 ? group_kernel_for<kFmtQ8, 512>(ups) : group_kernel_for<kFmtQ8, 256>(ups));
     // Every resident workgroup slot of the device, or fewer when the largest
