@@ -178,8 +178,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
 
 
 class MmhipError(RuntimeError):
-    def __init__(self, what: str, code: int):
-        msg = load_library().mmhip_last_error().decode(errors="replace")
+    def __init__(self, what: str, code: int, msg: Optional[str] = None):
+        if msg is None:
+            msg = load_library().mmhip_last_error().decode(errors="replace")
         super().__init__(f"{what} failed ({code}): {msg}")
         self.code = code
 
@@ -644,6 +645,37 @@ def plan_device_mask(ops) -> int:
 
 def op_schedule(op: int, backend: int, precision: int, estimated_us: int, sync_after: bool, shape=(0, 0, 0, 0)):
     return OpSchedule(op, backend, precision, int(sync_after), Shape(*shape), estimated_us)
+
+
+class PlanDispatch:
+    """The GPU side of HeteroExecutor.executeLayer (hetero_executor.zig:88-127,
+    the body dispatchGpu lacks at 154-159), as zig/hip_backend.zig's
+    PlanDispatch does: the device runs the whole moeFFN in one call, so
+    ffn_gate_up issues it for the token in `hidden`, siluMul is already done
+    inside it, and ffn_down hands the result back (hidden <- ffn_out,
+    inference.zig:1009). Other ops raise MmhipError with ERR_UNSUPPORTED (the
+    executor keeps them on its CPU path); siluMul or ffn_down without a
+    preceding ffn_gate_up raise it with ERR_INVALID."""
+
+    def __init__(self, moe: Optional["MoeLayer"], level: int = 0):
+        self.moe, self.level = moe, level
+        self.ffn_out = None
+
+    def dispatch_gpu(self, op: OpSchedule, hidden: np.ndarray) -> None:
+        if op.op == OP["ffn_gate_up"]:
+            if self.moe is None:
+                raise MmhipError("plan dispatch", ERR_UNSUPPORTED, "no MoE layer for ffn_gate_up")
+            self.ffn_out = self.moe.ffn(hidden, level=self.level)[0].reshape(hidden.shape)
+        elif op.op == OP["siluMul"]:
+            if self.ffn_out is None:
+                raise MmhipError("plan dispatch", ERR_INVALID, "siluMul before ffn_gate_up")
+        elif op.op == OP["ffn_down"]:
+            if self.ffn_out is None:
+                raise MmhipError("plan dispatch", ERR_INVALID, "ffn_down before ffn_gate_up")
+            hidden[...] = self.ffn_out
+            self.ffn_out = None
+        else:
+            raise MmhipError("plan dispatch", ERR_UNSUPPORTED, f"op {op.op} does not run on this backend")
 
 
 # ----------------------------------------------------------------------------
