@@ -9,11 +9,11 @@
 // LDS per K-chunk of up to 8 record units (2048 columns) as two int8 digit
 // planes per 32-column block (x ~ s (256 hi + lo)).
 //
-// Work items are (unit, tile) pairs in unit-major order, taken two tiles at a
-// time (tiles 2tp and 2tp + 1 of one unit) and split into 16 equal
-// contiguous runs of such pairs, one per wave, so a wave keeps one unit's
-// activation operands in registers while it walks tiles, and the two items
-// of a pair give it two independent MFMA chains. The A operands are sparse: for
+// Work items are (unit, tile) pairs in unit-major order, split into 16 equal
+// contiguous runs, one per wave, so a wave keeps one unit's activation
+// operands in registers while it walks tiles. The table reads of item i + 1
+// are issued before item i's arithmetic, so their latency overlaps it (two
+// sets of table words in registers). The A operands are sparse: for
 // the 16x16x64 MFMA of blocks 2j, 2j + 1 (lane group g's K range carries
 // the record of sub-block 2j, then that of 2j + 1, both at columns
 // 8g..8g+7) only the lanes whose A row m = 4i + e belongs to one of those
@@ -26,8 +26,7 @@
 //
 // B operands come from the 32 KiB LDS table keyed by b012 | P | idx (record
 // layout in device_common.hpp); the hi3 signs of the high dword come from an
-// 8-entry mask table and are applied with one xor-add. The table reads of both items of a pair are
-// issued before either is used.
+// 8-entry mask table and are applied with one xor-add.
 //
 // Each item leaves its 64 lane partial sums in LDS; after a chunk, every
 // output row adds its (unit, lane group) partials in a fixed order, so the
@@ -171,6 +170,7 @@ __device__ __forceinline__ v4i bpair(const long (&b)[8], int j) {
 template <int DEPTH, bool ROUTE, int NSEG>
 __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     constexpr int kRing = DEPTH + 1;
+    static_assert(kRing % 2 == 0, "two table-word sets alternate over the ring");
     // One LDS block with the table first: its byte offsets (below 32 KiB)
     // fold into the ds_read offset fields.
     struct Lds {
@@ -222,37 +222,32 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     // Sparse A row of this lane: block s_star of the unit, digit d_star.
     const uint32_t s_star = (n >> 2) + 4 * ((n >> 1) & 1u), d_star = n & 1u;
 
-    // Per-chunk state (set by start_chunk). Items are processed in pairs
-    // (tiles 2tp and 2tp + 1 of one unit, the second absent when the tile
-    // count is odd), so a pair never spans two units.
+    // Per-chunk state (set by start_chunk): items (unit ul, tile t), tp_n
+    // tiles per unit, this wave's items [p0, p1).
     uint32_t u0 = 0, uc = 1, tp_n = 1, p0 = 0, p1 = 0;
     auto start_chunk = [&](uint32_t chunk_u0, uint32_t units_in_chunk) {
         u0 = chunk_u0;
         uc = units_in_chunk;
-        tp_n = (n_tiles + 1) / 2;
+        tp_n = n_tiles;
         const uint32_t N = uc * tp_n;
         p0 = wave * N / kQWaves;
         p1 = (wave + 1) * N / kQWaves;
     };
     auto advance = [&](ItemPos q) { return (q.t + 1 == tp_n) ? ItemPos{q.ul + 1, 0} : ItemPos{q.ul, q.t + 1}; };
-    // Loads both items of pair q (ItemPos.t = pair index within the unit).
-    auto load = [&](bool valid, ItemPos q, uint4 (&r)[2], uint32_t (&dbits)[2]) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            uint32_t rs = kBufOob, ds = kBufOob;
-            const uint32_t tl = 2 * q.t + h;
-            if (valid && tl < n_tiles) {
-                const uint32_t tile = t_begin + tl, u = u0 + q.ul;
-                rs = tile * rec_tile + u * 1024;
-                ds = tile * d_tile + u * 2;
-            }
-            r[h] = buf_load_b128<kCacheStream>(rec_r, rec_voff, rs);
-            dbits[h] = buf_load_b16(d_r, d_voff, ds);  // cached: the tile's other units reuse the line
+    // Loads item q (ItemPos.t = tile within the range).
+    auto load = [&](bool valid, ItemPos q, uint4& r, uint32_t& dbits) {
+        uint32_t rs = kBufOob, ds = kBufOob;
+        if (valid) {
+            const uint32_t tile = t_begin + q.t, u = u0 + q.ul;
+            rs = tile * rec_tile + u * 1024;
+            ds = tile * d_tile + u * 2;
         }
+        r = buf_load_b128<kCacheStream>(rec_r, rec_voff, rs);
+        dbits = buf_load_b16(d_r, d_voff, ds);  // cached: the tile's other units reuse the line
     };
 
-    uint4 rb[kRing][2];
-    uint32_t db[kRing][2];
+    uint4 rb[kRing];
+    uint32_t db[kRing];
     ItemPos cur{0, 0}, nxt{0, 0};
     auto issue_first = [&]() {
         cur = ItemPos{p0 / tp_n, p0 % tp_n};
@@ -320,12 +315,18 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
         v4i av[4];
         float xa = 0.0f, xb = 0.0f, ha = 0.0f, hb = 0.0f;
         uint32_t a_ul = 0xFFFFFFFFu;
+        // Single items; the table reads of item i + 1 are issued before item
+        // i's arithmetic (two register sets, kRing even keeps the set of an
+        // item fixed at compile time).
+        RawB raw[2];
+        if (p0 < p1) fetch_b(rb[0], tab, mtab, raw[0]);
         for (uint32_t i = p0; i < p1; i += kRing) {
 #pragma unroll
             for (int q = 0; q < kRing; ++q) {
                 if (i + q < p1) {
                     load(i + q + DEPTH < p1, nxt, rb[(q + DEPTH) % kRing], db[(q + DEPTH) % kRing]);
                     nxt = advance(nxt);
+                    if (i + q + 1 < p1) fetch_b(rb[(q + 1) % kRing], tab, mtab, raw[(q + 1) & 1]);
                     if (cur.ul != a_ul) {
                         // This unit's sparse A operands and block scales.
                         a_ul = cur.ul;
@@ -342,32 +343,19 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
                         ha = xa * 0.5f;
                         hb = xb * 0.5f;
                     }
-                    // B operands of both items: all table reads first.
-                    RawB raw0, raw1;
-                    fetch_b(rb[q][0], tab, mtab, raw0);
-                    fetch_b(rb[q][1], tab, mtab, raw1);
-                    long b0[8], b1[8];
-                    finish_b(raw0, b0);
-                    finish_b(raw1, b1);
-                    v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+                    long b0[8];
+                    finish_b(raw[q & 1], b0);
+                    v4i acc = {0, 0, 0, 0};
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], bpair(b0, j), acc0, 0, 0, 0);
-                        acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], bpair(b1, j), acc1, 0, 0, 0);
-                    }
+                    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], bpair(b0, j), acc, 0, 0, 0);
                     // Blocks g and g + 4 of row n: d * (0.5 + ls) / 4 * s_x * digits.
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const v4i& acc = h ? acc1 : acc0;
-                        const uint4& r = rb[q][h];
-                        const float df = f16_scale(db[q][h]);
-                        const float sa = fmaf((float)iq2_ls_a(r), xa, ha);
-                        const float sb = fmaf((float)iq2_ls_b(r), xb, hb);
-                        float v = (float)digits_combine(acc[0], acc[1]) * sa;
-                        v = fmaf((float)digits_combine(acc[2], acc[3]), sb, v);
-                        const uint32_t tl = 2 * cur.t + h;
-                        if (tl < n_tiles) part[(cur.ul * n_tiles + tl) * 64 + lane] = v * df;
-                    }
+                    const uint4& r = rb[q];
+                    const float df = f16_scale(db[q]);
+                    const float sa = fmaf((float)iq2_ls_a(r), xa, ha);
+                    const float sb = fmaf((float)iq2_ls_b(r), xb, hb);
+                    float v = (float)digits_combine(acc[0], acc[1]) * sa;
+                    v = fmaf((float)digits_combine(acc[2], acc[3]), sb, v);
+                    part[(cur.ul * n_tiles + cur.t) * 64 + lane] = v * df;
                     cur = advance(cur);
                 }
             }
@@ -687,17 +675,19 @@ hipError_t launch_gemv_iq2(const GemvArgs* segs_in, uint32_t n_segs, int num_cu,
             if (gx > grid_x) grid_x = gx;
         }
     }
-    // Pairs in flight per wave: 2 (measured best), MMHIP_IQ2_DEPTH=3 to override.
+    // Items in flight per wave: 3 (the ring of record buffers is 4, even so
+    // that an item's table-word set is fixed at compile time); MMHIP_IQ2_DEPTH=5
+    // to override.
     static const int depth_env = env_int("MMHIP_IQ2_DEPTH", 0);
-    if (route) return launch_set<1>(segs, 1, reinterpret_cast<const void*>(&gemv_iq2_kernel<2, true, 1>), grid_x, s);
+    if (route) return launch_set<1>(segs, 1, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, true, 1>), grid_x, s);
     if (n == 1) {
-        const void* fn = depth_env == 3 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 1>)
-                                        : reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 1>);
+        const void* fn = depth_env == 5 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<5, false, 1>)
+                                        : reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 1>);
         return launch_set<1>(segs, 1, fn, grid_x, s);
     }
     if (n == 2)
-        return launch_set<2>(segs, 2, reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 2>), grid_x, s);
-    return launch_set<4>(segs, n, reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 4>), grid_x, s);
+        return launch_set<2>(segs, 2, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 2>), grid_x, s);
+    return launch_set<4>(segs, n, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 4>), grid_x, s);
 }
 
 hipError_t launch_down_combine_iq2(const DownCombineArgs& a, hipStream_t s) {
