@@ -274,19 +274,22 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG == 512) ? 4 : 2) void gro
     };
     next_run();
     {
-        // Small loads first and waited for: a CU returns loads in issue order
-        // across its waves, so weights issued first would hold them back.
+        // Small loads first: a CU returns loads in issue order across its
+        // waves, so weights issued earlier would hold them back. Every wave's
+        // small loads are issued (barrier) before the first weight loads go
+        // out; their latencies then overlap, and the LDS stores below wait
+        // only for the small loads.
         Iq2TableCopy<WG> tc;
         if (FMT == kFmtIq2) tc.load();
         uint2 lo[kPer], hi[kPer];
         float sc[kPerSc];
         stage_load(0, chunk_blk, lo, hi, sc);
-        vm_wait_all();
-        if (FMT == kFmtIq2) tc.store(tab);
-        stage_store(chunk_blk, lo, hi, sc);
+        __builtin_amdgcn_s_barrier();
         load(0, r0, d0);
         load(1, r1, d1);
         load(2, r2, d2);
+        if (FMT == kFmtIq2) tc.store(tab);
+        stage_store(chunk_blk, lo, hi, sc);
     }
     for (;;) {
         lds_barrier();
@@ -315,7 +318,7 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG == 512) ? 4 : 2) void gro
         uint2 lo[kPer], hi[kPer];
         float sc[kPerSc];
         stage_load(kb0, nb, lo, hi, sc);
-        if (kb0 == 0) vm_wait_all();  // a new item: small loads ahead of its weights
+        if (kb0 == 0) __builtin_amdgcn_s_barrier();  // a new item: every wave's small loads ahead of its weights
         load(0, r0, d0);
         load(1, r1, d1);
         load(2, r2, d2);
