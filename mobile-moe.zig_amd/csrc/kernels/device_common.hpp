@@ -80,9 +80,7 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 // Hardware conversion for scales that only feed products: exact for every
 // finite value (f16 denormals are enabled for these kernels); NaNs may come
 // out quieted, which cannot change a product that is NaN anyway.
-__device__ __forceinline__ float f16_scale(uint32_t h) {
-    return __half2float(__ushort_as_half((unsigned short)h));
-}
+__device__ __forceinline__ float f16_scale(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
 // Workgroup barrier that orders LDS only. __syncthreads() is a workgroup-
 // scope fence on all memory, which makes every wave wait for all of its
@@ -144,8 +142,8 @@ __device__ __forceinline__ uint32_t buf_load_b32(BufRsrc r, uint32_t voff, uint3
     return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL);
 }
 template <int POL = kCacheNormal>
-__device__ __forceinline__ uint32_t buf_load_b16(BufRsrc r, uint32_t voff, uint32_t soff) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, POL);
+__device__ __forceinline__ uint16_t buf_load_b16(BufRsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, POL);
 }
 
 __device__ __forceinline__ v4i mfma_i8(long a, long b) {

@@ -122,49 +122,45 @@ struct ItemPos {
     uint32_t ul, t;
 };
 
-// Raw table words of one record unit (lane's 8 records): .x = low dword,
-// .y = high dword before the hi3 signs; m: the hi3 sign masks (0xFF in each
-// byte to negate).
+// Table words of one record unit (the lane's 8 records): e[j] holds the
+// entries of records 2j and 2j + 1 side by side, which is the B operand of
+// the unit's j-th 16x16x64 MFMA once the hi3 signs are applied to words 1
+// and 3 in place; m[s]: record s's hi3 sign pair (below).
 struct RawB {
-    uint2 e[8];
+    v4i e[4];
     uint32_t m[8];
 };
 
+
 // Table words of the lane's 8 records (record layout in device_common.hpp):
-// the 8-byte entry keyed by the record's window; its high dword still needs
-// the hi3 signs.
-// The masks (one dword per hi3 value) are read from an 8-entry table: 64 lanes touch at most 8 addresses in 16 banks, so these
-// reads are broadcasts without bank conflicts, and they replace the four
-// VALU instructions that would build each mask.
+// the 8-byte entry keyed by the record's window, whose high word still needs
+// the hi3 signs, and the record's hi3 sign pair.
 __device__ __forceinline__ void fetch_b(const uint4& r, const uint32_t* tab, const uint32_t* mtab, RawB& raw) {
     const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
     const char* t8 = reinterpret_cast<const char*>(tab);
     const char* m8 = reinterpret_cast<const char*>(mtab);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const uint32_t d = w4[s >> 1];
-        raw.e[s] = *reinterpret_cast<const uint2*>(t8 + ((s & 1) ? ((d >> 15) & 0x7FF8u) : (d & 0x7FF8u)));
-        // hi3 of sub-block 2k + 1: bits 0..2; of 2k: bits 15..17 (times 4 bytes).
-        raw.m[s] = *reinterpret_cast<const uint32_t*>(m8 + (((s & 1) ? (d << 2) : (d >> 13)) & 0x1Cu));
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t d = w4[k];
+        // Record 2k: window at bits 3..14, hi3 at bits 15..17; record 2k + 1:
+        // window at bits 18..29, hi3 at bits 0..2.
+        const uint2 lo = *reinterpret_cast<const uint2*>(t8 + (d & 0x7FF8u));
+        const uint2 hi = *reinterpret_cast<const uint2*>(t8 + ((d >> 15) & 0x7FF8u));
+        raw.e[k] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+        raw.m[2 * k] = *reinterpret_cast<const uint32_t*>(m8 + ((d >> 13) & 0x1Cu));
+        raw.m[2 * k + 1] = *reinterpret_cast<const uint32_t*>(m8 + ((d << 2) & 0x1Cu));
     }
 }
 
-// B operands (signed int8 weights, 8 per record) from the table words.
-__device__ __forceinline__ void finish_b(const RawB& raw, long (&b)[8]) {
+// Applies the hi3 signs in place: raw.e[j] becomes the B operand of the
+// unit's j-th MFMA (K order: record 2j's bytes, then record 2j + 1's; the A
+// operand pairs its bytes the same way).
+__device__ __forceinline__ void finish_b(RawB& raw) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        // Bytes (b ^ 0xFF) + 1 = -b where the mask is set (|b| <= 0x2B: no carry).
-        const uint32_t hi = negate_bytes(raw.e[s].y, raw.m[s]);
-        b[s] = (long)(((uint64_t)hi << 32) | (uint64_t)raw.e[s].x);
+    for (int k = 0; k < 4; ++k) {
+        raw.e[k][1] = (int)negate_bytes((uint32_t)raw.e[k][1], raw.m[2 * k]);
+        raw.e[k][3] = (int)negate_bytes((uint32_t)raw.e[k][3], raw.m[2 * k + 1]);
     }
-}
-
-// B operand of a 16x16x64 MFMA: the records of sub-blocks 2j and 2j + 1
-// (K = 16g..16g+7 and 16g+8..16g+15 of lane group g; the A operand pairs
-// its bytes the same way).
-__device__ __forceinline__ v4i bpair(const long (&b)[8], int j) {
-    const uint64_t l = (uint64_t)b[2 * j], h = (uint64_t)b[2 * j + 1];
-    return v4i{(int)(uint32_t)l, (int)(uint32_t)(l >> 32), (int)(uint32_t)h, (int)(uint32_t)(h >> 32)};
 }
 
 template <int DEPTH, bool ROUTE, int NSEG>
@@ -235,7 +231,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     };
     auto advance = [&](ItemPos q) { return (q.t + 1 == tp_n) ? ItemPos{q.ul + 1, 0} : ItemPos{q.ul, q.t + 1}; };
     // Loads item q (ItemPos.t = tile within the range).
-    auto load = [&](bool valid, ItemPos q, uint4& r, uint32_t& dbits) {
+    auto load = [&](bool valid, ItemPos q, uint4& r, uint16_t& dbits) {
         uint32_t rs = kBufOob, ds = kBufOob;
         if (valid) {
             const uint32_t tile = t_begin + q.t, u = u0 + q.ul;
@@ -247,7 +243,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     };
 
     uint4 rb[kRing];
-    uint32_t db[kRing];
+    uint16_t db[kRing];
     ItemPos cur{0, 0}, nxt{0, 0};
     auto issue_first = [&]() {
         cur = ItemPos{p0 / tp_n, p0 % tp_n};
@@ -343,11 +339,11 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
                         ha = xa * 0.5f;
                         hb = xb * 0.5f;
                     }
-                    long b0[8];
-                    finish_b(raw[q & 1], b0);
+                    finish_b(raw[q & 1]);
                     v4i acc = {0, 0, 0, 0};
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], bpair(b0, j), acc, 0, 0, 0);
+                    for (int j = 0; j < 4; ++j)
+                        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], raw[q & 1].e[j], acc, 0, 0, 0);
                     // Blocks g and g + 4 of row n: d * (0.5 + ls) / 4 * s_x * digits.
                     const uint4& r = rb[q];
                     const float df = f16_scale(db[q]);
@@ -508,7 +504,7 @@ __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineA
     __builtin_amdgcn_s_barrier();
     // Weight items of this wave: item i = p * units + u, i = wave + kDcWaves j.
     uint4 rb[kDcItemsPerWave];
-    uint32_t db[kDcItemsPerWave];
+    uint16_t db[kDcItemsPerWave];
     const uint32_t rec_voff = lane * 16, d_voff = n * a.d_row * 2;
 #pragma unroll
     for (uint32_t j = 0; j < kDcItemsPerWave; ++j) {
@@ -557,11 +553,10 @@ __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineA
             av[q] = v4i{(int)(lo ? xw.x : 0u), (int)(lo ? xw.y : 0u), (int)(hi ? xw.x : 0u), (int)(hi ? xw.y : 0u)};
         }
         const float xa = lds.xs[i * 8 + g] * 0.25f, xb4 = lds.xs[i * 8 + g + 4] * 0.25f;
-        long b[8];
-        finish_b(raw, b);
+        finish_b(raw);
         v4i acc = {0, 0, 0, 0};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], bpair(b, q), acc, 0, 0, 0);
+        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], raw.e[q], acc, 0, 0, 0);
         const float sa = fmaf((float)iq2_ls_a(rb[j]), xa, xa * 0.5f);
         const float sb = fmaf((float)iq2_ls_b(rb[j]), xb4, xb4 * 0.5f);
         float v = (float)digits_combine(acc[0], acc[1]) * sa;
