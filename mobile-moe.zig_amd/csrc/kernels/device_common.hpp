@@ -199,12 +199,16 @@ __device__ __forceinline__ uint32_t iq2_ls_a(const uint4& r) { return (r.x >> 30
 __device__ __forceinline__ uint32_t iq2_ls_b(const uint4& r) { return (r.z >> 30) | ((r.w >> 30) << 2); }
 
 // All eight 4-bit ls values of the lane's row (nibble s = sub-block s),
-// gathered from the row's four lanes.
+// gathered from the row's four lanes (lane groups g = 0..3) by OR-ing over
+// 16-lane rows with two permlane swaps: permlane16_swap(m, m) returns rows
+// (0,0,2,2) and (1,1,3,3) of m, permlane32_swap(m, m) rows (0,1,0,1) and
+// (2,3,2,3). No LDS traffic.
 __device__ __forceinline__ uint32_t iq2_ls_all(const uint4& r, uint32_t g) {
-    uint32_t mine = (iq2_ls_a(r) << (4 * g)) | (iq2_ls_b(r) << (16 + 4 * g));
-    mine |= __shfl_xor(mine, 16, kWave);
-    mine |= __shfl_xor(mine, 32, kWave);
-    return mine;
+    const uint32_t mine = (iq2_ls_a(r) << (4 * g)) | (iq2_ls_b(r) << (16 + 4 * g));
+    const auto p = __builtin_amdgcn_permlane16_swap(mine, mine, false, false);
+    const uint32_t pair = p[0] | p[1];
+    const auto q = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
+    return q[0] | q[1];
 }
 
 // Exact integer value of one MFMA output for the (hi, lo) digit rows:
