@@ -212,7 +212,7 @@ def stream_section(ctx, ev, gib=4, reps=10):
     rk.free()
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"read_GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(us, 1),
-            "workload": f"plain streaming read of {gib} GiB (16-byte non-temporal loads, 4 in flight per thread)"}
+            "workload": f"plain streaming read of {gib} GiB (short-lived waves, four 16-byte non-temporal loads per thread)"}
 
 
 def calibration_reads(ctx, n=3, mib=512):
