@@ -533,6 +533,41 @@ def kv_codec_section(ctx, ev, rng, reps=20, n_rows=131072, row_len=576):
     return out
 
 
+def dequant_section(ctx, ev, rng, orc, reps=20, n_mats=16):
+    """dequantize (dequant.zig:632-659) of raw GGUF blocks on the device:
+    n_mats expert matrices [1536 x 2048] of Q8_0 (dequantizeQ8_0Slice,
+    133-142) and of IQ2_XXS (dequantizeIQ2XXS, 358-369) to f32 in one call
+    each; rates in algorithmic bytes (raw blocks in, f32 out). The CPU line is
+    the oracle's dequantize of one such matrix on one core (the reference
+    dequantizes the whole f32 matrix before each IQ2_XXS GEMV)."""
+    out = {"workload": f"{n_mats} x [{INTER} x {HIDDEN}] raw GGUF blocks -> f32, one call per type"}
+    st = ctx.stream
+    n = n_mats * INTER * HIDDEN
+    od = mm.DeviceArray(ctx, n * 4)
+    for name, fmt in (("q8_0", mm.Q8_0), ("iq2_xxs", mm.IQ2_XXS)):
+        raw = mm.make_weight(rng, fmt, INTER, HIDDEN, n_mats)
+        rd = mm.DeviceArray.from_numpy(ctx, raw)
+        for _ in range(3):
+            ctx.dequantize_dev(od, rd, fmt, n)
+        ctx.synchronize()
+        us = ev.per_call_us(st, lambda i: ctx.dequantize_dev(od, rd, fmt, n), reps)
+        nbytes = raw.nbytes + n * 4
+        gbs = nbytes / (us * 1e-6) / 1e9
+        r = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
+        if orc is not None:
+            one = raw[: raw.nbytes // n_mats]
+            m = INTER * HIDDEN
+            ref = orc.dequantize(one, fmt, m)
+            got = od.to_numpy(np.float32, m)
+            r["bit_exact_first_matrix"] = bool(np.array_equal(got.view(np.uint32), ref.view(np.uint32)))
+            cus, runs = cpu_time_us(lambda: orc.dequantize(one, fmt, m))
+            r["cpu"] = {"us_per_matrix": round(cus, 1), "threads": 1, "runs": runs}
+        rd.free()
+        out[name] = r
+    od.free()
+    return out
+
+
 def cpu_kv_codec_baseline(rng, seconds=2.0, row_len=576):
     """Oracle quantizeQ8_0 per row on one core (KVCache.put's loop), bounded sample."""
     orc = oracle()
@@ -700,7 +735,7 @@ def main():
     ap.add_argument("--cpu-moe-tokens", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle (parity and CPU baselines)")
     ap.add_argument("--only", default=None,
-                    help="run one section: stream, step, cfg0, cfg1, cfg2, cfg3, cfg4, q8step, kv, logits, mla")
+                    help="run one section: stream, step, cfg0, cfg1, cfg2, cfg3, cfg4, q8step, kv, dequant, logits, mla")
     ap.add_argument("--pmc-summary", default=None, metavar="DIR",
                     help="summarise a rocprofv3 --pmc output directory and exit")
     args = ap.parse_args()
@@ -740,6 +775,8 @@ def main():
             res = moe_section(ctx, ev, rng, max(50, args.steps), None, orc, which=(1,) if only == "cfg3" else (64,))[0]
         elif only == "kv":
             res = kv_codec_section(ctx, ev, rng)
+        elif only == "dequant":
+            res = dequant_section(ctx, ev, rng, orc)
         elif only == "logits":
             res = logits_section(ctx, ev, rng, args.pool_gib)
         elif only == "mla":
@@ -825,6 +862,7 @@ def main():
         "host": host_info(),
     }
     out["kv_q8_codec"] = kv_codec_section(ctx, ev, rng)
+    out["dequantize"] = dequant_section(ctx, ev, rng, orc)
     out["logits"] = logits_section(ctx, ev, rng, args.pool_gib)
     out["mla"] = mla_section(ctx, ev, rng, args.pool_gib)
     if not args.no_cpu:

@@ -26,29 +26,41 @@ __global__ void dequant_q8_0_kernel(const uint8_t* __restrict__ raw, uint64_t n,
     out[i] = d * (float)(int8_t)blk[2 + (i & 31)];
 }
 
-// IQ2_XXS (dequant.zig:316-369): one thread per 8-weight group.
-__global__ void dequant_iq2_kernel(const uint8_t* __restrict__ raw, uint64_t n, float* __restrict__ out) {
-    uint64_t grp = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    uint64_t base = grp * 8;
+// IQ2_XXS (dequant.zig:316-369): one thread per half of an 8-weight group,
+// so that consecutive lanes write consecutive 16 bytes: one non-temporal
+// float4 store per thread (whole cache lines per instruction) when out is
+// 16-byte aligned.
+__global__ void dequant_iq2_kernel(const uint8_t* __restrict__ raw, uint64_t n, bool vec, float* __restrict__ out) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t base = t * 4;
     if (base >= n) return;
-    uint64_t sb = base >> 8;
-    uint32_t ib = (uint32_t)((base >> 5) & 7);
-    uint32_t l = (uint32_t)((base >> 3) & 3);
+    const uint32_t h = (uint32_t)(t & 1);
+    const uint64_t sb = base >> 8;
+    const uint32_t ib = (uint32_t)((base >> 5) & 7);
+    const uint32_t l = (uint32_t)((base >> 3) & 3);
     const uint8_t* blk = raw + sb * 66;
-    float d = f16_bits_to_f32(ld16(blk));
-    uint32_t a0 = ld32u(blk + 2 + 8 * ib);
-    uint32_t a1 = ld32u(blk + 2 + 8 * ib + 4);
-    float db = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
-    uint64_t gv = c_iq2_grid[(a0 >> (8 * l)) & 0xFFu];
-    uint32_t code = (a1 >> (7 * l)) & 0x7Fu;
-    uint32_t s = code | ((uint32_t)(__popc(code) & 1) << 7);
+    const float d = f16_bits_to_f32(ld16(blk));
+    const uint32_t a0 = ld32u(blk + 2 + 8 * ib);
+    const uint32_t a1 = ld32u(blk + 2 + 8 * ib + 4);
+    const float db = d * (0.5f + (float)(a1 >> 28)) * 0.25f;
+    const uint64_t gv = c_iq2_grid[(a0 >> (8 * l)) & 0xFFu];
+    const uint32_t code = (a1 >> (7 * l)) & 0x7Fu;
+    const uint32_t sg = code | ((uint32_t)(__popc(code) & 1) << 7);
+    float v[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        if (base + j < n) {
-            float mag = (float)((gv >> (8 * j)) & 0xFFu);
-            float sign = ((s >> j) & 1u) ? -1.0f : 1.0f;
-            out[base + j] = db * mag * sign;
-        }
+    for (uint32_t e = 0; e < 4; ++e) {
+        const uint32_t j = 4 * h + e;
+        const float mag = (float)((gv >> (8 * j)) & 0xFFu);
+        const float sign = ((sg >> j) & 1u) ? -1.0f : 1.0f;
+        v[e] = db * mag * sign;
+    }
+    if (vec && base + 4 <= n) {
+        typedef float v4f_ __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(v4f_{v[0], v[1], v[2], v[3]}, reinterpret_cast<v4f_*>(out + base));
+    } else {
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e)
+            if (base + e < n) out[base + e] = v[e];
     }
 }
 
@@ -424,11 +436,16 @@ hipError_t launch_dequant(const void* raw, uint32_t type, uint64_t n, float* out
             dequant_f16_kernel<<<(unsigned)((n + bs - 1) / bs), bs, 0, s>>>((const uint16_t*)raw, n, out);
             break;
         case kTypeQ8_0:
+            // As one row of n values (the KV codec's dequantiser: float4
+            // non-temporal stores) where its limits allow.
+            if ((reinterpret_cast<uintptr_t>(raw) & 1u) == 0 && n <= 0xFFFFFFFFull)
+                return launch_dequantize_q8_0_rows(raw, 1, (uint32_t)n, out, (n + 3) & ~3ull, s);  // one row: the stride is unused
             dequant_q8_0_kernel<<<(unsigned)((n + bs - 1) / bs), bs, 0, s>>>((const uint8_t*)raw, n, out);
             break;
         case kTypeIq2: {
-            uint64_t groups = (n + 7) / 8;
-            dequant_iq2_kernel<<<(unsigned)((groups + bs - 1) / bs), bs, 0, s>>>((const uint8_t*)raw, n, out);
+            const uint64_t quads = (n + 3) / 4;
+            const bool vec = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+            dequant_iq2_kernel<<<(unsigned)((quads + bs - 1) / bs), bs, 0, s>>>((const uint8_t*)raw, n, vec, out);
             break;
         }
         default:
