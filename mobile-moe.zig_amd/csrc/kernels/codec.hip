@@ -276,11 +276,12 @@ struct RowBlock {
     uint32_t blk;
 };
 __device__ __forceinline__ RowBlock row_block(uint64_t row0, uint32_t blk0, uint32_t k, uint32_t bpr, float inv_bpr) {
+    // 24-bit multiplies (full rate): t < 2^24 and bpr < 2^24 here.
     const uint32_t t = blk0 + k;
     uint32_t q = (uint32_t)((float)t * inv_bpr);
-    if (q * bpr > t) --q;
-    if ((q + 1) * bpr <= t) ++q;
-    return RowBlock{row0 + q, t - q * bpr};
+    if (__umul24(q, bpr) > t) --q;
+    if (__umul24(q + 1, bpr) <= t) ++q;
+    return RowBlock{row0 + q, t - __umul24(q, bpr)};
 }
 
 __global__ __launch_bounds__(kQ8Threads) void quantize_q8_0_rows_kernel(const float* __restrict__ x,
@@ -340,27 +341,32 @@ __global__ __launch_bounds__(kQ8Threads) void quantize_q8_0_rows_kernel(const fl
             // the exact quotient (rcp: 1 ulp; |x/d| <= 127.00002), and the
             // correctly rounded quotient is within 2^-17 of it; where z is
             // more than 1e-4 from every half-integer both round to the same
-            // integer. Lanes with a value closer (or a non-finite z: d = 0,
-            // Inf or NaN inputs) redo their block with the IEEE division.
+            // integer. Lanes with a value closer, with |z| > 127.25 (a
+            // subnormal d can push the quotient past 127.5, which the exact
+            // path clamps) or with a non-finite z (d = 0, Inf or NaN inputs)
+            // redo their block with the IEEE division.
             const float rd = __builtin_amdgcn_rcpf(d);
-            float r[4];
+            uint32_t q4 = 0;
             bool near = false;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float z = v[u][e] * rd, az = fabsf(z);
-                near |= !(az <= 128.0f) || fabsf((az - truncf(az)) - 0.5f) <= 1.0e-4f;
-                r[e] = copysignf(truncf(az + 0.5f), z);
+                // y = |z| + 0.5 (rounding error <= 2^-18 for |z| < 128): |z| is
+                // near a half-integer where y is near an integer.
+                const float z = v[u][e] * rd, az = fabsf(z), y = az + 0.5f, r = truncf(y);
+                near |= !(az <= 127.25f) || !(fabsf((y - r) - 0.5f) < 0.5f - 1.0e-4f);
+                // Not near: |z| <= 127.25 and away from half-integers, so the
+                // rounded value is in [-127, 127]; absent values are 0.
+                q4 |= ((uint32_t)(int)copysignf(r, z) & 0xFFu) << (8 * e);
             }
             if (__any(near) && near) {
+                q4 = 0;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) r[e] = roundf(v[u][e] / d);
-            }
-            uint32_t q4 = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float re = (r[e] == r[e] && d > 0.0f && (uint32_t)e < n_live[u]) ? r[e] : 0.0f;  // NaN input (@intFromFloat traps)
-                const int q = (int)fminf(fmaxf(re, -127.0f), 127.0f);
-                q4 |= (uint32_t)(q & 0xFF) << (8 * e);
+                for (int e = 0; e < 4; ++e) {
+                    const float r = roundf(v[u][e] / d);
+                    const float re = (r == r && d > 0.0f && (uint32_t)e < n_live[u]) ? r : 0.0f;  // NaN input (@intFromFloat traps)
+                    const int q = (int)fminf(fmaxf(re, -127.0f), 127.0f);
+                    q4 |= (uint32_t)(q & 0xFF) << (8 * e);
+                }
             }
             const uint32_t kk = k + kQ8Groups * u;
             if (b0 + kk < nblk) {
