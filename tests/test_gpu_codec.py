@@ -238,6 +238,25 @@ def test_q8_0_near_ties_match_oracle(ctx, orc, max_abs):
         dx.free(); db.free()
 
 
+@pytest.mark.parametrize("max_abs", [1.0e-37, 1.0e-39, 1.0e-41, 1.0e-43, 3.0e-45])
+def test_q8_0_subnormal_scales_match_oracle(ctx, orc, max_abs):
+    """Blocks whose scale d = max|x| / 127 is an f32 subnormal, with values
+    next to half-integer quotients: d loses precision there, so quotients can
+    pass 127.5 (clamped) and the fast quotient's bounds are exercised."""
+    x = _near_tie_rows(max_abs)
+    rng = np.random.default_rng(17)
+    x[::3, :31] = (rng.uniform(-1.0, 1.0, (x[::3].shape[0], 31)) * np.float32(max_abs)).astype(np.float32)
+    n_rows, row_len = x.shape
+    ref = orc.quantize_q8_0_rows(x, row_len)
+    dx = mm.DeviceArray.from_numpy(ctx, x)
+    db = mm.DeviceArray(ctx, ref.size + 4)
+    try:
+        ctx.quantize_q8_0_rows_dev(db, dx, row_len, n_rows, row_len)
+        np.testing.assert_array_equal(db.to_numpy(np.uint8, ref.size), ref)
+    finally:
+        dx.free(); db.free()
+
+
 @pytest.mark.parametrize("scale", [1.0, 1e-4, 50.0])
 def test_q8_0_large_random_match_oracle(ctx, orc, scale):
     n_rows, row_len = 7000, 576
