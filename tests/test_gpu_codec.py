@@ -83,6 +83,30 @@ def test_dequant_dev_twin_matches_host_path(ctx, orc):
     dout.free()
 
 
+@pytest.mark.parametrize("fmt,raw_off,out_off", [(mm.Q8_0, 1, 4), (mm.Q8_0, 2, 0), (mm.IQ2_XXS, 1, 4),
+                                                  (mm.IQ2_XXS, 0, 8)])
+def test_dequant_dev_misaligned_pointers(ctx, orc, fmt, raw_off, out_off):
+    """mmhip_dequantize_dev with raw blocks at odd / 2-byte offsets and an
+    output that is not 16-byte aligned (the scalar-store and 2-byte-load
+    paths), against the oracle bit for bit."""
+    rng = np.random.default_rng(raw_off * 10 + out_off)
+    n = 3 * 256 + 64
+    raw = mm.make_weight(rng, fmt, 1, ((n + 255) // 256) * 256)
+    buf = np.zeros(raw.size + 16, np.uint8)
+    buf[raw_off:raw_off + raw.size] = raw
+    draw = mm.DeviceArray.from_numpy(ctx, buf)
+    dout = mm.DeviceArray(ctx, n * 4 + 64)
+    try:
+        mm.check(ctx.lib.mmhip_dequantize_dev(ctx.handle, dout.ptr + out_off, draw.ptr + raw_off, fmt, n),
+                 "mmhip_dequantize_dev")
+        ctx.synchronize()
+        got = dout.to_numpy(np.uint8, n * 4 + out_off)[out_off:].view(np.float32)
+        _same_bits(got, orc.dequantize(raw, fmt, n))
+    finally:
+        draw.free()
+        dout.free()
+
+
 def test_unsupported_type_is_an_error(ctx):
     with pytest.raises(mm.MmhipError) as e:
         ctx.dequantize(np.zeros(144, np.uint8), 12, 256)   # Q4_K: not on this path
