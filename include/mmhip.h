@@ -85,7 +85,7 @@ int mmhip_num_cu(mmhip_ctx* ctx);
 /* Kernel timing: when enabled, HIP events are recorded on the context's
  * stream around every launch of the hot kernels; mmhip_profile_read sums
  * them per kernel family ("gemv_q", "gemv_float", "qmm", "quantize",
- * "moe_router", "moe_route", "moe_quantize", "moe_gateup", "moe_down",
+ * "moe_router", "moe_route", "moe_quantize", "moe_gateup", "moe_down", "moe_decode",
  * "moe_combine"). This fills the role
  * of the per-op GPU timings the reference leaves empty
  * (op_perf_db.zig:88-97). Enabling resets the accumulators. */

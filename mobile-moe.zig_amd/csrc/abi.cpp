@@ -110,6 +110,15 @@ int mmhip_init(mmhip_ctx** out_ctx, int device) {
         delete ctx;
         return hip_fail(e, "init: scratch symbol address");
     }
+    e = hipHostMalloc((void**)&ctx->status, sizeof(uint32_t), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&ctx->status_dev, ctx->status, 0);
+    if (e != hipSuccess) {
+        if (ctx->status) (void)hipHostFree(ctx->status);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_fail(e, "init: status word");
+    }
+    *ctx->status = 0;
     *out_ctx = ctx;
     return MMHIP_OK;
 }
@@ -128,13 +137,15 @@ void mmhip_destroy(mmhip_ctx* ctx) {
     ctx->h_in.release();
     ctx->h_out.release();
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    if (ctx->status) (void)hipHostFree(ctx->status);
     delete ctx;
 }
 
 int mmhip_synchronize(mmhip_ctx* ctx) {
     if (int rc = require_ctx(ctx)) return rc;
     hipError_t e = hipStreamSynchronize(ctx->stream);
-    return e == hipSuccess ? MMHIP_OK : hip_fail(e, "synchronize");
+    if (e != hipSuccess) return hip_fail(e, "synchronize");
+    return check_device_status(ctx, "synchronize");
 }
 
 void* mmhip_stream(mmhip_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }

@@ -25,6 +25,15 @@ int hip_fail(hipError_t e, const char* what) {
     return MMHIP_ERR_HIP;
 }
 
+int check_device_status(mmhip_ctx* ctx, const char* what) {
+    const uint32_t st = ctx->status ? __atomic_load_n(ctx->status, __ATOMIC_ACQUIRE) : 0u;
+    if (st == 0) return MMHIP_OK;
+    __atomic_store_n(ctx->status, 0u, __ATOMIC_RELEASE);
+    set_error(MMHIP_ERR_HIP, std::string(what) + ": decode MoE launch: a grid-wide wait timed out (code " +
+                                 std::to_string(st) + "); its output is invalid");
+    return MMHIP_ERR_HIP;
+}
+
 uint64_t block_size(uint32_t type) {
     switch (type) {
         case kF32: case kF16: return 1;

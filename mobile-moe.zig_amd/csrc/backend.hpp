@@ -82,6 +82,10 @@ struct mmhip_ctx {
     mmhip::DevBuf d_arg;  // argmax partials (value, index) of the first pass
     mmhip::HostBuf h_in, h_out;
     void* noalloc = nullptr;  // this device's fixed QMM scratch (mmhip_qmm_dev_noalloc)
+    // Pinned host word that device code sets when a grid-wide wait of the
+    // one-launch decode MoE layer timed out (0: none); read after a sync.
+    uint32_t* status = nullptr;
+    uint32_t* status_dev = nullptr;
     KernelTimer timer;
 };
 
@@ -100,6 +104,11 @@ struct TimedLaunch {
 };
 
 namespace mmhip {
+
+// MMHIP_OK, or MMHIP_ERR_HIP with a message when device code recorded a
+// failure in the context's status word since the last check (which clears
+// it). Call after the context's stream has been synchronised.
+int check_device_status(mmhip_ctx* ctx, const char* what);
 
 // Upload helpers shared by the ABI and the MoE layer.
 int weight_create(mmhip_ctx* ctx, const void* raw, bool raw_on_device, uint32_t type, uint64_t rows,

@@ -124,9 +124,13 @@ __device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
 }
 // Cache policy of a load: kCacheNormal, or kCacheStream (non-temporal) for
 // data read exactly once (weights), so that it does not evict the small
-// shared data (activations, grid) that every workgroup reads.
+// shared data (activations, grid) that every workgroup reads. kCacheDevice
+// (sc1, device scope) reads data that another XCD's workgroup wrote during
+// the same launch: each XCD has its own L2, and a plain load could return a
+// line that L2 still holds from before the write.
 constexpr int kCacheNormal = 0;
 constexpr int kCacheStream = 2;
+constexpr int kCacheDevice = 16;
 template <int POL = kCacheNormal>
 __device__ __forceinline__ uint4 buf_load_b128(BufRsrc r, uint32_t voff, uint32_t soff) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL);

@@ -34,6 +34,7 @@
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "route_ops.hpp"
+#include "iq2_ops.hpp"
 
 namespace mmhip {
 
@@ -46,19 +47,6 @@ constexpr uint32_t kQChunkBlocks = kQChunkUnits * 8;  // 32-column blocks per ch
 constexpr uint32_t kQMaxTiles = 64;                  // row tiles per workgroup
 constexpr uint32_t kQMaxItems = 384;                 // (unit, tile) items per workgroup and chunk
 
-// Quantises 4 columns per lane (8 lanes per 32-column block, quantize_quad)
-// into the chunk's digit planes: aq[(b * 2 + digit) * 32 + column].
-__device__ __forceinline__ void x_store_planes(const float (&v)[4], uint32_t nblk, uint32_t b0, uint8_t* aq,
-                                               float* xs) {
-    uint32_t h4, l4;
-    const float s = quantize_quad(v, h4, l4);
-    const uint32_t b = b0 + (threadIdx.x >> 3), jq = threadIdx.x & 7;
-    if (b < nblk) {
-        *reinterpret_cast<uint32_t*>(aq + b * 64 + 4 * jq) = h4;
-        *reinterpret_cast<uint32_t*>(aq + b * 64 + 32 + 4 * jq) = l4;
-        if (jq == 0) xs[b] = s;
-    }
-}
 
 // Activation columns [c0, c0 + 32 nblk) of the problem's vector (times
 // silu(x) * u when silu_mul) into the digit planes; 128 blocks per pass.
@@ -122,46 +110,6 @@ struct ItemPos {
     uint32_t ul, t;
 };
 
-// Table words of one record unit (the lane's 8 records): e[j] holds the
-// entries of records 2j and 2j + 1 side by side, which is the B operand of
-// the unit's j-th 16x16x64 MFMA once the hi3 signs are applied to words 1
-// and 3 in place; m[s]: record s's hi3 sign pair (below).
-struct RawB {
-    v4i e[4];
-    uint32_t m[8];
-};
-
-
-// Table words of the lane's 8 records (record layout in device_common.hpp):
-// the 8-byte entry keyed by the record's window, whose high word still needs
-// the hi3 signs, and the record's hi3 sign pair.
-__device__ __forceinline__ void fetch_b(const uint4& r, const uint32_t* tab, const uint32_t* mtab, RawB& raw) {
-    const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
-    const char* t8 = reinterpret_cast<const char*>(tab);
-    const char* m8 = reinterpret_cast<const char*>(mtab);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t d = w4[k];
-        // Record 2k: window at bits 3..14, hi3 at bits 15..17; record 2k + 1:
-        // window at bits 18..29, hi3 at bits 0..2.
-        const uint2 lo = *reinterpret_cast<const uint2*>(t8 + (d & 0x7FF8u));
-        const uint2 hi = *reinterpret_cast<const uint2*>(t8 + ((d >> 15) & 0x7FF8u));
-        raw.e[k] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
-        raw.m[2 * k] = *reinterpret_cast<const uint32_t*>(m8 + ((d >> 13) & 0x1Cu));
-        raw.m[2 * k + 1] = *reinterpret_cast<const uint32_t*>(m8 + ((d << 2) & 0x1Cu));
-    }
-}
-
-// Applies the hi3 signs in place: raw.e[j] becomes the B operand of the
-// unit's j-th MFMA (K order: record 2j's bytes, then record 2j + 1's; the A
-// operand pairs its bytes the same way).
-__device__ __forceinline__ void finish_b(RawB& raw) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        raw.e[k][1] = (int)negate_bytes((uint32_t)raw.e[k][1], raw.m[2 * k]);
-        raw.e[k][3] = (int)negate_bytes((uint32_t)raw.e[k][3], raw.m[2 * k + 1]);
-    }
-}
 
 template <int DEPTH, bool ROUTE, int NSEG>
 __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
@@ -427,13 +375,6 @@ constexpr uint32_t kDcMaxUnits = 8;  // inner width <= 2048
 constexpr uint32_t kDcMaxItems = kDcMaxProbs * kDcMaxUnits;
 constexpr uint32_t kDcItemsPerWave = (kDcMaxItems + kDcWaves - 1) / kDcWaves;
 
-// silu(x) = x / (1 + e^-x) (math.zig:38-41) with the hardware exp2 and
-// reciprocal (a few ulp from the correctly rounded quotient): each workgroup
-// here forms every expert's activation, so the IEEE division and expf would
-// dominate its arithmetic.
-__device__ __forceinline__ float silu_fast(float x) {
-    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
-}
 
 __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineArgs a) {
     struct Lds {
@@ -547,30 +488,11 @@ __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineA
     }
     lds_barrier();
 
-    const uint32_t s_star = (n >> 2) + 4 * ((n >> 1) & 1u), d_star = n & 1u;
 #pragma unroll
     for (uint32_t j = 0; j < kDcItemsPerWave; ++j) {
         const uint32_t i = wave + kDcWaves * j;
         if (i >= n_items) break;
-        RawB raw;
-        fetch_b(rb[j], lds.tab, lds.mtab, raw);
-        const uint2 xw = *reinterpret_cast<const uint2*>(lds.aq + ((i * 8 + s_star) * 2 + d_star) * 32 + 8 * g);
-        v4i av[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const bool lo = s_star == 2u * q, hi = s_star == 2u * q + 1;
-            av[q] = v4i{(int)(lo ? xw.x : 0u), (int)(lo ? xw.y : 0u), (int)(hi ? xw.x : 0u), (int)(hi ? xw.y : 0u)};
-        }
-        const float xa = lds.xs[i * 8 + g] * 0.25f, xb4 = lds.xs[i * 8 + g + 4] * 0.25f;
-        finish_b(raw);
-        v4i acc = {0, 0, 0, 0};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[q], raw.e[q], acc, 0, 0, 0);
-        const float sa = fmaf((float)iq2_ls_a(rb[j]), xa, xa * 0.5f);
-        const float sb = fmaf((float)iq2_ls_b(rb[j]), xb4, xb4 * 0.5f);
-        float v = (float)digits_combine(acc[0], acc[1]) * sa;
-        v = fmaf((float)digits_combine(acc[2], acc[3]), sb, v);
-        lds.part[i * 64 + lane] = v * f16_scale(db[j]);
+        lds.part[i * 64 + lane] = iq2_item(rb[j], db[j], lds.aq + i * 8 * 64, lds.xs + i * 8, lds.tab, lds.mtab, n, g);
     }
     lds_barrier();
     if (threadIdx.x < 16 * kDcMaxProbs) {

@@ -169,6 +169,36 @@ struct DownCombineArgs {
 };
 hipError_t launch_down_combine_iq2(const DownCombineArgs& a, hipStream_t s);
 
+// One-launch decode MoE layer for IQ2_XXS experts (decode_moe.hip): router,
+// routing, gate/up, down and combine of one token in one cooperative launch
+// of num_cu workgroups. Matrices: gate e / up E + e / shared gate 2E / shared
+// up 2E + 1 in gu_*, down e / shared down E in dn_*.
+struct DecodeMoeArgs {
+    RouteArgs route;            // n_tokens 1; scores: the router's output [E]
+    const void* router_w;       // [E][hidden], f32 (router_type 0) or f16 (1)
+    uint32_t router_type;
+    const float* x;             // hidden vector [hidden]
+    uint32_t hidden, inter;     // multiples of 256, at most 2048
+    const uint4* gu_recs;
+    const uint16_t* gu_dvals;
+    uint64_t gu_rec_stride, gu_d_stride;
+    uint32_t gu_d_row;
+    const uint4* dn_recs;
+    const uint16_t* dn_dvals;
+    uint64_t dn_rec_stride, dn_d_stride;
+    uint32_t dn_d_row;
+    uint8_t* hq;                // [5][inter / 32][64] digit planes of silu(gate) * up
+    float* hs;                  // [5][inter / 32] their block scales
+    uint64_t* score_tags;       // [n_experts] (epoch << 32 | score bits), published by the router rows
+    uint32_t* h_flags;          // [5][inter / 32] epoch of the call whose h block is published
+    uint32_t epoch;             // this call's number, never 0; the buffers above start zeroed
+    uint32_t* status;           // host-visible word: nonzero when a grid wait timed out
+    const float* bias;          // deferral bias [hidden] or null
+    float* out;                 // [hidden]
+};
+bool decode_moe_iq2_fits(uint32_t hidden, uint32_t inter, uint32_t n_experts, int num_cu);
+hipError_t launch_decode_moe_iq2(const DecodeMoeArgs& a, int num_cu, hipStream_t s);
+
 // Allocation-free QMM scratch (noalloc.hip): kNoallocScratchBytes of device
 // memory per device, kept until the process ends. noalloc_scratch() returns
 // this device's address; call it with `device` current. Every call on a

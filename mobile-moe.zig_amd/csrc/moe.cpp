@@ -3,6 +3,9 @@
 // (src/scheduler.zig:169-262) and forwardBatch's per-token loop (346-351).
 //
 // One call enqueues, on the context stream:
+//   T == 1 with IQ2_XXS experts (shared expert merged or absent): the whole
+//   layer as one cooperative launch (decode_moe.hip)          "moe_decode"
+//   otherwise:
 //   router scores   f32/f16 GEMV, [T][E]                     "moe_router"
 //   T > 1: route    heap top-k, softmax, throttle, counts,
 //                   slot layout and problem lists            "moe_route"
@@ -24,6 +27,7 @@
 //   combine         weighted sum in route order + shared
 //                   + deferral bias                           "moe_combine"
 // No routing result returns to the host in between.
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -69,6 +73,14 @@ struct mmhip_moe_layer {
     void* xq_d = nullptr;    // quantised down input [5 T][dn cols_pad]
     void* xq_sd = nullptr;   // quantised shared down input [T][sh_dn cols_pad]
     float* bias = nullptr;   // [hidden]
+    // One-launch decode (IQ2_XXS experts): h planes and scales handed from
+    // the gate/up workgroups to the down workgroups, and the grid counters.
+    uint8_t* dm_hq = nullptr;   // [5][inter / 32][64]
+    float* dm_hs = nullptr;     // [5][inter / 32]
+    uint64_t* dm_scores = nullptr;  // [n_experts] epoch-tagged router scores
+    uint32_t* dm_flags = nullptr;   // [5][inter / 32] epoch-tagged h blocks
+    uint32_t dm_epoch = 0;          // number of the last one-launch call (never 0 once called)
+    bool decode_fused = false;  // the layer's decode calls use the one-launch kernel
     float* d_in = nullptr;   // host-ABI staging [T][hidden]
     float* d_out = nullptr;
 };
@@ -138,6 +150,10 @@ size_t carve(mmhip_moe_layer* L, char* base) {
     L->xq_d = take(quant_act_bytes(S, L->dn->geom.cols_pad));
     if (L->has_shared && !L->shared_merged) L->xq_sd = take(quant_act_bytes(T, L->sh_dn->geom.cols_pad));
     L->bias = (float*)take(H * 4);
+    L->dm_hq = (uint8_t*)take(5 * (uint64_t)(I / 32) * 64);
+    L->dm_hs = (float*)take(5 * (uint64_t)(I / 32) * 4);
+    L->dm_scores = (uint64_t*)take((uint64_t)L->n_experts * 8);
+    L->dm_flags = (uint32_t*)take(5 * (uint64_t)(I / 32) * 4);
     L->d_in = (float*)take(T * H * 4);
     L->d_out = (float*)take(T * H * 4);
     return off;
@@ -216,7 +232,8 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
     r.work_dn = L->work_dn;
     r.n_work = L->n_work;
     r.inter = I;
-    {
+    const bool fused = T == 1 && L->decode_fused;
+    if (!fused) {
         TimedLaunch tl(ctx, "moe_router");
         MOE_TRY(check_hip(launch_gemv_float(L->router->plain, L->router_type, 0, hidden, H, L->scores, E, T, E, H, s),
                           "moe: router"));
@@ -238,6 +255,39 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
         }
         TimedLaunch tl(ctx, "moe_route");
         MOE_TRY(check_hip(launch_route(r, s), "moe: route"));
+    }
+    if (fused) {
+        // Decode in one launch: router, routing, gate/up, down and combine.
+        const TileGeom& gg = L->gu->geom;
+        const TileGeom& gd = L->dn->geom;
+        DecodeMoeArgs d{};
+        d.route = r;
+        d.router_w = L->router->plain;
+        d.router_type = L->router_type;
+        d.x = hidden;
+        d.hidden = H;
+        d.inter = I;
+        d.gu_recs = L->gu->recs;
+        d.gu_dvals = L->gu->dvals;
+        d.gu_rec_stride = gg.rec_stride;
+        d.gu_d_stride = gg.d_stride;
+        d.gu_d_row = (uint32_t)gg.d_row;
+        d.dn_recs = L->dn->recs;
+        d.dn_dvals = L->dn->dvals;
+        d.dn_rec_stride = gd.rec_stride;
+        d.dn_d_stride = gd.d_stride;
+        d.dn_d_row = (uint32_t)gd.d_row;
+        d.hq = L->dm_hq;
+        d.hs = L->dm_hs;
+        d.score_tags = L->dm_scores;
+        d.h_flags = L->dm_flags;
+        if (++L->dm_epoch == 0) L->dm_epoch = 1;
+        d.epoch = L->dm_epoch;
+        d.status = ctx->status_dev;
+        d.bias = with_bias ? L->bias : nullptr;
+        d.out = out;
+        TimedLaunch tl(ctx, "moe_decode");
+        return check_hip(launch_decode_moe_iq2(d, ctx->num_cu, s), "moe: one-launch decode");
     }
     if (T == 1) {
         // Decode: the gate/up GEMV routes the token itself (no routing launch).
@@ -441,6 +491,13 @@ int mmhip_moe_layer_create(mmhip_ctx* ctx, const mmhip_moe_weights* wts, mmhip_m
         return hip_fail(e, "moe_layer_create: scratch");
     }
     carve(L, static_cast<char*>(L->scratch));
+    // Decode calls run as one launch when the experts are IQ2_XXS, the
+    // shared expert (if any) is merged, and the shapes fit the kernel;
+    // MMHIP_DECODE_FUSED=0 selects the three-launch sequence instead.
+    const char* fused_env = getenv("MMHIP_DECODE_FUSED");
+    L->decode_fused = !(fused_env && fused_env[0] == '0') && L->gu->geom.fmt == kFmtIq2 &&
+                      L->dn->geom.fmt == kFmtIq2 && (!has_shared || L->shared_merged) &&
+                      decode_moe_iq2_fits(L->hidden, L->inter, L->n_experts, ctx->num_cu);
     *out_layer = L;
     return MMHIP_OK;
 }
@@ -508,6 +565,7 @@ int mmhip_moe_ffn(mmhip_ctx* ctx, mmhip_moe_layer* layer, const float* hidden_ho
                        "moe_ffn: route weights");
     const hipError_t e = hipStreamSynchronize(s);
     if (rc == MMHIP_OK && e != hipSuccess) rc = hip_fail(e, "moe_ffn: synchronize");
+    if (rc == MMHIP_OK) rc = check_device_status(ctx, "moe_ffn");
     if (rc == MMHIP_OK && ctx->timer.on) ctx->timer.drain();
     return rc == MMHIP_OK ? (int)k : rc;
 }
