@@ -41,10 +41,12 @@
 //     value and whether it belongs to this call;
 //   - an h block is written with device-scope stores; once they are performed
 //     (s_waitcnt vmcnt(0)), its flag word is set to the epoch. Consumers poll
-//     the flags with device-scope loads and then read the blocks with plain
-//     loads, which the XCD's L2 shares between its workgroups: nothing in the
-//     launch reads a block before its flag is set, and lines cached by
-//     earlier launches are invalidated at the launch boundary.
+//     the flags with device-scope loads and then read the blocks' digit
+//     planes with plain loads, which the XCD's L2 shares between its
+//     workgroups: nothing in the launch reads a plane line before every
+//     block on it is published, and lines cached by earlier launches are
+//     invalidated at the launch boundary. The block scales (several
+//     problems' to a line) are read with device-scope loads.
 // The memory model's agent-scope release/acquire fences write back and
 // invalidate the whole L2 per use, and a single shared counter serialises
 // hundreds of atomics; both cost several microseconds per hand-over here.
@@ -204,9 +206,10 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
 
     // ---- Router row loads first (the routing waits on them): row r on
     // workgroup G - E + r, the last workgroups, which have no shared-expert
-    // job. Other workgroups' resources are empty (the loads read zeros
-    // without a memory access), so every load is issued unconditionally and
-    // the compiler's load counters stay exact.
+    // job (vector loads return in issue order, so a job's weight loads would
+    // hold the row's loads back). Other workgroups' resources are empty (the
+    // loads read zeros without a memory access), so every load is issued
+    // unconditionally and the compiler's load counters stay exact.
     const bool router_wg = w >= G - E;
     const uint32_t r_row = router_wg ? w - (G - E) : 0;
     const bool f16_router = a.router_type != 0;
@@ -448,52 +451,63 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
 
     // ---- Down projection and combine of row tile dt.
     if (dt < dn_tiles) {
-        if (wave == 0) {
-            // Flags of jobs lane + 64 q (at most 5 per lane).
-            constexpr int kQ = (kDmMaxHBlocks + 63) / 64;
-            struct Flags {
-                uint32_t v[kQ];
-            } fa;
-            grid_wait(
-                fa,
-                [&](Flags& f) {
+        auto stage = [&](uint32_t j0, uint32_t j1) {
+            // Jobs [j0, j1) (whole problems): wait for their flags (wave 0),
+            // copy their h planes and scales into LDS, then the down items of
+            // their problems. The planes are read with plain loads: they are
+            // published, each problem's planes fill whole 128-byte lines
+            // (nbh * 64 bytes), and no line of them was cached before. The
+            // scales are read with device-scope loads: one line holds several
+            // problems' scales, so a plain load of some problems' scales
+            // could cache a line that other problems' scales are later
+            // written to (a first stage over the shared expert's blocks,
+            // measured slower, did exactly that).
+            if (wave == 0) {
+                constexpr int kQ = (kDmMaxHBlocks + 63) / 64;  // flags per lane, at most
+                struct Flags {
+                    uint32_t v[kQ];
+                } fa;
+                grid_wait(
+                    fa,
+                    [&](Flags& f) {
 #pragma unroll
-                    for (int q = 0; q < kQ; ++q) {
-                        const uint32_t jj = lane + 64 * q;
-                        f.v[q] = jj < n_jobs
-                                     ? __hip_atomic_load(a.h_flags + jj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                     : epoch;
-                    }
-                },
-                [&](const Flags& f) {
-                    bool ok = true;
+                        for (int q = 0; q < kQ; ++q) {
+                            const uint32_t jj = j0 + lane + 64 * q;
+                            f.v[q] = jj < j1 ? __hip_atomic_load(a.h_flags + jj, __ATOMIC_RELAXED,
+                                                                 __HIP_MEMORY_SCOPE_AGENT)
+                                             : epoch;
+                        }
+                    },
+                    [&](const Flags& f) {
+                        bool ok = true;
 #pragma unroll
-                    for (int q = 0; q < kQ; ++q) ok = ok && f.v[q] == epoch;
-                    return __all(ok) != 0;
-                },
-                a.status, 2u);
-        }
-        lds_barrier();
-        {
-            // Every problem's h planes and scales into LDS (plain loads: the
-            // blocks are published and no line of them was cached before).
-            const uint32_t nblk = P * nbh;
-            const BufRsrc qr = make_rsrc(a.hq, nblk * 64);
-            for (uint32_t o = threadIdx.x * 16; o < nblk * 64; o += kDmWg * 16)
-                *reinterpret_cast<uint4*>(lds.hq + o) = buf_load_b128(qr, o, 0);
-            const BufRsrc sr = make_rsrc(a.hs, nblk * 4);
-            if (threadIdx.x < nblk) lds.hs[threadIdx.x] = __uint_as_float(buf_load_b32(sr, threadIdx.x * 4, 0));
-        }
-        lds_barrier();
-#pragma unroll
-        for (uint32_t s = 0; s < kDmDownPerWave; ++s) {
-            const uint32_t i = (wave - 1) + kDmDownWaves * s;
-            if (wave > 0 && i < n_dn_items) {
-                const float v = item_rows(
-                    iq2_item(rb_dn[s], db_dn[s], lds.hq + i * 8 * 64, lds.hs + i * 8, lds.tab, lds.mtab, n, g));
-                if (lane < 16) lds.rows_dn[i * 16 + lane] = v;
+                        for (int q = 0; q < kQ; ++q) ok = ok && f.v[q] == epoch;
+                        return __all(ok) != 0;
+                    },
+                    a.status, 2u);
             }
-        }
+            lds_barrier();
+            const BufRsrc qr = make_rsrc(a.hq + (uint64_t)j0 * 64, (j1 - j0) * 64);
+            for (uint32_t o = threadIdx.x * 16; o < (j1 - j0) * 64; o += kDmWg * 16)
+                *reinterpret_cast<uint4*>(lds.hq + j0 * 64 + o) = buf_load_b128(qr, o, 0);
+            const BufRsrc sr = make_rsrc(a.hs + j0, (j1 - j0) * 4);
+            if (threadIdx.x < j1 - j0)
+                lds.hs[j0 + threadIdx.x] = __uint_as_float(buf_load_b32<kCacheDevice>(sr, threadIdx.x * 4, 0));
+            lds_barrier();
+            // Items i = p * du + u of these jobs' problems (j0, j1 are whole
+            // problems: multiples of nbh = 8 du).
+            const uint32_t i0 = j0 / 8, i1 = j1 / 8;
+#pragma unroll
+            for (uint32_t s = 0; s < kDmDownPerWave; ++s) {
+                const uint32_t i = (wave - 1) + kDmDownWaves * s;
+                if (wave > 0 && i >= i0 && i < i1) {
+                    const float v = item_rows(
+                        iq2_item(rb_dn[s], db_dn[s], lds.hq + i * 8 * 64, lds.hs + i * 8, lds.tab, lds.mtab, n, g));
+                    if (lane < 16) lds.rows_dn[i * 16 + lane] = v;
+                }
+            }
+        };
+        stage(0, n_jobs);
         lds_barrier();
         if (threadIdx.x < 16 * P) {
             // Row r of problem p: the decode GEMV's row sum (units in order).
