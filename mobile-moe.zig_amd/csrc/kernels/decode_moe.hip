@@ -74,7 +74,6 @@ constexpr uint32_t kDmDownWaves = kDmWaves - 1;
 constexpr uint32_t kDmDownPerWave = (kDmDownItems + kDmDownWaves - 1) / kDmDownWaves;
 constexpr uint32_t kDmMaxHBlocks = kDmMaxProbs * kDmMaxUnits * 8;  // 32-element blocks of every problem's h
 constexpr uint32_t kDmRouterRow = kDmMaxUnits * 256 / 4 + 4;        // one chain's terms, padded (banks)
-constexpr uint32_t kSpinLimit = 1u << 22;
 
 static_assert(kDmJobItems % kDmWaves == 0, "job items split evenly over the waves");
 
@@ -104,13 +103,14 @@ __device__ __forceinline__ void publish_u32(uint32_t* p, uint32_t v) {
 // into v, done(v) tells whether everything it read is published. One round
 // is in flight at a time: a second one issued ahead would still be in
 // flight on return, and the next use of its registers would wait for it.
-// After kSpinLimit rounds the wait gives up and records `code`.
+// After 1 + limit rounds the wait gives up and records `code`.
 template <typename V, typename Load, typename Done>
-__device__ __forceinline__ void grid_wait(V& v, Load load, Done done, uint32_t* status, uint32_t code) {
+__device__ __forceinline__ void grid_wait(V& v, Load load, Done done, uint32_t limit, uint32_t* status,
+                                          uint32_t code) {
     for (uint32_t spins = 0;; ++spins) {
         load(v);
         if (done(v)) return;
-        if (spins >= kSpinLimit) {
+        if (spins >= limit) {
             if (status) __hip_atomic_store(status, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             return;
         }
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
                 for (int q = 0; q < 4; ++q) ok = ok && (uint32_t)(t.v[q] >> 32) == epoch;
                 return __all(ok) != 0;
             },
-            a.status, 1u);
+            a.spin_limit, a.status, 1u);
         float sc[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) sc[q] = __uint_as_float((uint32_t)ta.v[q]);
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
                         for (int q = 0; q < kQ; ++q) ok = ok && f.v[q] == epoch;
                         return __all(ok) != 0;
                     },
-                    a.status, 2u);
+                    a.spin_limit, a.status, 2u);
             }
             lds_barrier();
             const BufRsrc qr = make_rsrc(a.hq + (uint64_t)j0 * 64, (j1 - j0) * 64);

@@ -146,3 +146,59 @@ def test_one_launch_decode_many_calls_in_a_row(ctx):
         os_.free()
         fused.free()
         split.free()
+
+
+@pytest.mark.parametrize("n_exp,shared,router_type", [(128, True, mm.F32), (256, False, mm.F16)])
+def test_one_launch_decode_many_experts(ctx, orc, n_exp, shared, router_type):
+    """128 and 256 routed experts (top-k over 2 or 4 score slots per lane),
+    hidden 1024, width 512."""
+    rng = np.random.default_rng(730 + n_exp)
+    H, I = 1024, 512
+    router, gate, up, down, sh = _weights(rng, H, I, n_exp, shared, router_type=router_type)
+    fused, split, kw = _pair(ctx, H, I, n_exp, router, gate, up, down, sh, router_type=router_type)
+    bias = rng.normal(0.0, 0.5, H).astype(np.float32)
+    try:
+        _run_pair(ctx, orc, fused, split, kw, rng, [(0, 0), (0, 0), (2, 0), (3, 4)], H, bias)
+    finally:
+        fused.free()
+        split.free()
+
+
+def test_one_launch_decode_wait_timeout_is_reported(ctx):
+    """A grid-wide wait that gives up is reported, not silent: with
+    MMHIP_DECODE_SPIN_LIMIT=0 each wait polls once, so workgroups that reach
+    the routing before the router rows are published give up (the launch
+    still ends). The call returns the HIP error code with the reason, the
+    context's status is cleared, and a layer with the default limit then
+    matches the three-launch path."""
+    rng = np.random.default_rng(740)
+    H, I, E = 2048, 1536, 64
+    router, gate, up, down, sh = _weights(rng, H, I, E, True)
+    kw = dict(hidden=H, inter=I, n_experts=E, expert_type=mm.IQ2_XXS, router=router, gate=gate, up=up, down=down,
+              shared=sh, shared_inter=I, shared_type=mm.IQ2_XXS)
+    prev = os.environ.pop("MMHIP_DECODE_SPIN_LIMIT", None)
+    os.environ["MMHIP_DECODE_SPIN_LIMIT"] = "0"
+    try:
+        hasty = mm.MoeLayer(ctx, **kw)
+    finally:
+        os.environ.pop("MMHIP_DECODE_SPIN_LIMIT", None)
+        if prev is not None:
+            os.environ["MMHIP_DECODE_SPIN_LIMIT"] = prev
+    fused, split, _ = _pair(ctx, H, I, E, router, gate, up, down, sh)
+    try:
+        errors = []
+        for _ in range(10):
+            h = rng.standard_normal((1, H)).astype(np.float32)
+            try:
+                hasty.ffn(h)
+            except mm.MmhipError as e:
+                errors.append(e)
+        assert errors, "no wait gave up with a limit of one poll"
+        assert all(e.code == -4 and "grid-wide wait" in str(e) for e in errors), errors[0]
+        ctx.synchronize()  # the status word was cleared by the call that reported it
+        h = rng.standard_normal((1, H)).astype(np.float32)
+        _same_bits(fused.ffn(h)[0], split.ffn(h)[0])
+    finally:
+        hasty.free()
+        fused.free()
+        split.free()
