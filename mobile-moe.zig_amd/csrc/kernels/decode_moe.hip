@@ -362,7 +362,12 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
     }
 
     // ---- Routing, by wave 0 of every workgroup: scores e = lane + 64 q
-    // (experts past E read as published zeros and are never selected).
+    // (experts past E read as published zeros and are never selected). The
+    // selected ids and which of them are computed go to every wave at once;
+    // the route weights (softmax over the selected logits), needed only by
+    // the combine, follow while the weight loads are in flight.
+    uint32_t r_ids[kMaxK];
+    float r_ts[kMaxK];
     if (wave == 0) {
         struct Tags {
             uint64_t v[4];
@@ -388,18 +393,18 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
         float sc[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) sc[q] = __uint_as_float((uint32_t)ta.v[q]);
-        const TokenRoute tr = route_scores(a.route, sc);
-        if (w == 0 && lane == 0) decode_route_outputs(a.route, tr);
+        route_select(a.route, sc, r_ids, r_ts);
+        uint32_t act, deferred;
+        route_active(a.route, act, deferred);
         if (lane == 0) {
             uint32_t na = 0;
 #pragma unroll
             for (uint32_t i = 0; i < kMaxK; ++i) {
-                lds.route[2 + i] = tr.ids[i];
-                lds.route[2 + kMaxK + i] = __float_as_uint(tr.w[i]);
-                if (i < a.route.k && ((tr.act >> i) & 1u)) lds.route_e[na++] = tr.ids[i];
+                lds.route[2 + i] = r_ids[i];
+                if (i < a.route.k && ((act >> i) & 1u)) lds.route_e[na++] = r_ids[i];
             }
-            lds.route[0] = tr.act;
-            lds.route[1] = tr.deferred;
+            lds.route[0] = act;
+            lds.route[1] = deferred;
             lds.route_n = na;
         }
     }
@@ -415,6 +420,16 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
         const bool run = j_r < n_jobs;
         const uint32_t e = lds.route_e[run ? p_r - sh : 0];
         job_issue(run, e, E + e, js_r, rb_gu, db_gu);
+    }
+    if (wave == 0) {
+        // The route weights (read by the combine, after later barriers) and,
+        // by workgroup 0, the routing outputs.
+        const TokenRoute tr = finish_route(a.route, r_ids, r_ts);
+        if (w == 0 && lane == 0) decode_route_outputs(a.route, tr);
+        if (lane == 0) {
+#pragma unroll
+            for (uint32_t i = 0; i < kMaxK; ++i) lds.route[2 + kMaxK + i] = __float_as_uint(tr.w[i]);
+        }
     }
     // The job's items, then wave 0 publishes h, then waves 1..15 issue the
     // down tile's loads (needed only after the next hand-over). A CU takes

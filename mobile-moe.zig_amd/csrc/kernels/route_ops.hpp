@@ -173,6 +173,16 @@ __device__ inline void load_scores(const RouteArgs& a, uint32_t t, float (&sc)[4
     for (int q = 0; q < 4; ++q) sc[q] = __uint_as_float(buf_load_b32(sr, (lane + 64 * q) * 4, 0));
 }
 
+// Which of the k selected experts are computed (bit i: assignment i) and
+// whether the others are deferred: all of them, except under the heavy
+// throttle, which keeps the top expert only (scheduler.zig:225-242). Known
+// from the ids alone, before the weights.
+__device__ __forceinline__ void route_active(const RouteArgs& a, uint32_t& act, uint32_t& deferred) {
+    const bool heavy = a.level == 3 && a.k > 1;
+    act = heavy ? 1u : (1u << a.k) - 1u;
+    deferred = heavy ? 1u : 0u;
+}
+
 // Route weights of the selected experts (ids, logits ts in topK order).
 __device__ inline TokenRoute finish_route(const RouteArgs& a, const uint32_t (&ids)[kMaxK], const float (&ts)[kMaxK]) {
     const uint32_t k = a.k;
@@ -199,10 +209,8 @@ __device__ inline TokenRoute finish_route(const RouteArgs& a, const uint32_t (&i
         if (i < k) r.w[i] = r.w[i] * a.scale;
     // Heavy throttle keeps the top expert only and renormalises it
     // (225-242); the others are deferred.
-    r.act = (1u << k) - 1u;
-    if (a.level == 3 && k > 1) {
-        r.act = 1u;
-        r.deferred = 1;
+    route_active(a, r.act, r.deferred);
+    if (r.deferred) {
         const float rem = 0.0f + r.w[0];
         if (rem > 0.0f) r.w[0] = r.w[0] * (a.scale / rem);
     }
@@ -261,13 +269,25 @@ __device__ inline bool top_k_distinct64(float v, uint32_t n, uint32_t k, uint32_
     return true;
 }
 
-// Routing of one token by a whole wave (scores one per lane).
-__device__ inline TokenRoute route_scores(const RouteArgs& a, const float (&sc)[4]) {
-    uint32_t ids[kMaxK] = {0, 0, 0, 0};
-    float ts[kMaxK] = {0.f, 0.f, 0.f, 0.f};
+// The k selected experts of one token and their logits in topK order, by a
+// whole wave (scores one per lane).
+__device__ inline void route_select(const RouteArgs& a, const float (&sc)[4], uint32_t (&ids)[kMaxK],
+                                    float (&ts)[kMaxK]) {
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxK; ++i) {
+        ids[i] = 0;
+        ts[i] = 0.0f;
+    }
     const bool fast = a.n_experts <= 64 ? top_k_distinct64(sc[0], a.n_experts, a.k, ids, ts)
                                         : top_k_distinct(sc, a.n_experts, a.k, ids, ts);
     if (!fast) top_k_wave(sc, a.n_experts, a.k, ids, ts);
+}
+
+// Routing of one token by a whole wave (scores one per lane).
+__device__ inline TokenRoute route_scores(const RouteArgs& a, const float (&sc)[4]) {
+    uint32_t ids[kMaxK];
+    float ts[kMaxK];
+    route_select(a, sc, ids, ts);
     return finish_route(a, ids, ts);
 }
 
