@@ -56,7 +56,7 @@ constexpr int kIq2UnitCols = 256;
 constexpr int kQ8UnitCols = 64;
 constexpr float kDigitMax = 32512.0f;  // 127 * 256: hi digit stays in [-127, 127]
 constexpr int kIq2TableWords = 8192;   // 4096 record entries of two u32
-constexpr int kIq2MaskWords = 8;       // hi3 sign masks, after the record entries in LDS
+constexpr int kIq2MaskWords = 16;      // hi3 sign masks (mask, mask & 0x01010101), after the record entries
 constexpr int kIq2LdsWords = kIq2TableWords + kIq2MaskWords;
 // LDS A layout (decode): per 256-column group, lane (m = 0|1, g) owns a
 // 64-byte run holding the 8 A operands (8 x 8 digits) of the group's 8
@@ -181,21 +181,24 @@ __host__ __device__ constexpr uint32_t negate_bytes(uint32_t w, uint32_t mask) {
 __host__ __device__ constexpr uint32_t iq2_hi3_mask(uint32_t h) { return nibble_byte_mask(h | (parity3(h) << 3)); }
 
 // IQ2_XXS B operands of the two records in one tile dword, from the LDS
-// record entries and hi3 masks (tab: kIq2LdsWords words). The mask reads
-// touch at most 8 words: broadcasts without bank conflicts.
+// record entries and hi3 masks (tab: kIq2LdsWords words). The mask table
+// holds 8 entries (mask, mask & 0x01010101) keyed by hi3, so the signs cost
+// one xor-add, (w ^ m) + (m & 0x01010101) (negate_bytes with the second term
+// read instead of computed). The mask reads touch at most 16 words:
+// broadcasts without bank conflicts.
 __device__ __forceinline__ long iq2_bop(uint32_t entry_off, uint32_t mask_off, const uint32_t* __restrict__ tab) {
     const char* t8 = reinterpret_cast<const char*>(tab);
     const uint2 e = *reinterpret_cast<const uint2*>(t8 + entry_off);
-    const uint32_t m = *reinterpret_cast<const uint32_t*>(t8 + kIq2TableWords * 4 + mask_off);
-    return (long)(((uint64_t)negate_bytes(e.y, m) << 32) | (uint64_t)e.x);
+    const uint2 m = *reinterpret_cast<const uint2*>(t8 + kIq2TableWords * 4 + mask_off);
+    return (long)(((uint64_t)((e.y ^ m.x) + m.y) << 32) | (uint64_t)e.x);
 }
 // Sub-block 2k: entry at bits 3..14, hi3 at bits 15..17.
 __device__ __forceinline__ long iq2_bop_lo(uint32_t d, const uint32_t* __restrict__ tab) {
-    return iq2_bop(d & 0x7FF8u, (d >> 13) & 0x1Cu, tab);
+    return iq2_bop(d & 0x7FF8u, (d >> 12) & 0x38u, tab);
 }
 // Sub-block 2k + 1: entry at bits 18..29, hi3 at bits 0..2.
 __device__ __forceinline__ long iq2_bop_hi(uint32_t d, const uint32_t* __restrict__ tab) {
-    return iq2_bop((d >> 15) & 0x7FF8u, (d << 2) & 0x1Cu, tab);
+    return iq2_bop((d >> 15) & 0x7FF8u, (d << 3) & 0x38u, tab);
 }
 
 // ls of sub-block g (from dwords 0,1) and 4+g (dwords 2,3) of this lane.
@@ -266,7 +269,10 @@ struct Iq2TableCopy {
     __device__ __forceinline__ void store(uint32_t* tab) const {
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) reinterpret_cast<uint4*>(tab)[threadIdx.x + WG * i] = v[i];
-        if (threadIdx.x < kIq2MaskWords) tab[kIq2TableWords + threadIdx.x] = iq2_hi3_mask(threadIdx.x);
+        if (threadIdx.x < kIq2MaskWords) {
+            const uint32_t m = iq2_hi3_mask(threadIdx.x >> 1);
+            tab[kIq2TableWords + threadIdx.x] = (threadIdx.x & 1) ? m & 0x01010101u : m;
+        }
     }
 };
 
