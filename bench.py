@@ -8,7 +8,12 @@ the batch-1 GEMV of a GLM-4.7-Flash-shaped layer's routed experts:
 weights rotating over distinct device copies (> 1 GiB, several times the
 256 MiB Infinity Cache), so every step streams its weights from HBM. The step
 time and the kernel durations come from the same timed pass: HIP events are
-recorded around every launch of it on the library's stream.
+recorded around every launch of it on the library's stream. Every timed pass
+(here and in the sections below) follows SETTLE_S seconds of continuous work
+on its own calls, then the warm-up calls: from idle, the GPU's clocks and
+power take tens of milliseconds of work to settle, and a serving GPU runs
+settled. The first 20 headline steps from idle are reported beside the
+result (`roofline.settle`).
 
 `configs` holds one object per workload of the path, each with its device
 time, GB/s of algorithmic bytes, fraction of the 8 TB/s peak and of the
@@ -53,6 +58,7 @@ import mmhip as mm  # noqa: E402
 
 METRIC = "quant GEMV HBM GB/s (% of peak) + MoE FFN layer µs/token at batch 1 and 64"
 HBM_PEAK_GBS = 8000.0
+SETTLE_S = 0.25  # seconds of continuous work on a timed pass's own calls before it (HipEvents.settle)
 HIDDEN, INTER, EXPERTS = 2048, 1536, 64
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq2_traffic.txt")
 GIB = 1 << 30
@@ -69,6 +75,7 @@ class HipEvents:
         self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
         self.pool = []
 
     def _get(self, n):
@@ -98,10 +105,30 @@ class HipEvents:
         self.hip.hipEventSynchronize(b)
         return self.elapsed_ms(a, b)
 
+    def settle(self, stream, call, seconds=None):
+        """Runs call(i) back to back for `seconds` (SETTLE_S) before a timed
+        pass. From idle, the MI355X's clocks and power settle over the first
+        tens of milliseconds of continuous work: the headline step measured
+        ~23 µs for its first ~60 steps, up to ~32 µs around step 160, and
+        ~22.9 µs again after ~800 steps (and at 22.8 µs after 0.3 s of
+        work). A serving GPU runs settled, so the timed passes follow this.
+        Returns the number of calls made."""
+        seconds = SETTLE_S if seconds is None else seconds
+        t0 = time.perf_counter()
+        i = 0
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(32):
+                call(i)
+                i += 1
+            self.hip.hipStreamSynchronize(ctypes.c_void_p(stream))
+        return i
+
     def per_call_us(self, stream, call, n_per_block, blocks=5):
         """Median over `blocks` blocks of n back-to-back calls (call(i), i
-        running on across blocks): µs per call."""
+        running on across blocks), after the GPU has settled on the same
+        calls: µs per call."""
         k = [0]
+        self.settle(stream, call)
 
         def block():
             for _ in range(n_per_block):
@@ -255,11 +282,16 @@ def step_section(ctx, ev, fmt, steps, warmup, pool_gib, rng):
 
     b_gate = gemv_bytes(fmt, INTER, HIDDEN, EXPERTS, True)
     b_down = gemv_bytes(fmt, HIDDEN, INTER, EXPERTS, False)
+    st = ctx.stream
+    # The first 20 steps from idle (reported, not the result), then the
+    # settle phase, the warm-up steps and the timed steps.
+    ctx.synchronize()
+    first_us = ev.time_ms(st, lambda: [step(i) for i in range(20)]) * 1e3 / 20
+    settle_steps = ev.settle(st, step)
     for i in range(warmup):
         step(i)
     ctx.synchronize()
     a, b = ev._get(2)
-    st = ctx.stream
     t0 = time.perf_counter()
     ev.record(a, st)
     for i in range(steps):
@@ -284,7 +316,8 @@ def step_section(ctx, ev, fmt, steps, warmup, pool_gib, rng):
     for arr in (x, xd, yg, yd):
         arr.free()
     return {"step_bytes": b_gate + b_down, "b_gate": b_gate, "b_down": b_down, "dt": dt, "n_sets": n_sets,
-            "pool_gib": n_sets * per_set / GIB, "device_us_per_step": device_us, "separate_launches": sep}
+            "pool_gib": n_sets * per_set / GIB, "device_us_per_step": device_us, "separate_launches": sep,
+            "first_20_steps_us": first_us, "settle_steps": settle_steps}
 
 
 def read_traffic():
@@ -418,10 +451,12 @@ def moe_section(ctx, ev, rng, calls, stream_gbs, orc, n_layers=8, n_tokens=61, w
         def run(i):
             layers[i % n_layers].ffn_dev(hs[i % len(hs)], od, t)
 
+        ev.settle(stream, run)
         for i in range(2 * n_layers):
             run(i)
         ctx.synchronize()
         cold = ev.time_ms(stream, lambda: [run(i) for i in range(n)]) / n * 1e3 / t
+        ev.settle(stream, lambda i: layers[0].ffn_dev(hs[0], od, t))
         for _ in range(5):
             layers[0].ffn_dev(hs[0], od, t)
         ctx.synchronize()
@@ -849,6 +884,10 @@ def main():
             "bytes_per_step": g["step_bytes"],
             "frac_of_stream": round(achieved / sgbs, 4),
             "timing": "HIP events around the timed pass of ms_per_step (back-to-back launches, one per step)",
+            "settle": {"seconds": SETTLE_S, "steps": g["settle_steps"],
+                       "first_20_steps_us": round(g["first_20_steps_us"], 3),
+                       "note": "the timed pass follows the settle steps and the warm-up steps; the first 20 steps "
+                               "from idle run while the GPU's clocks and power settle (not the result)"},
             "separate_launches": g["separate_launches"],
         },
         "stream": stream,
