@@ -288,8 +288,10 @@ __global__ __launch_bounds__(kFloatThreads) void gemv_strict_kernel(const WT* __
                                                                     uint32_t n_vecs, uint32_t rows, uint32_t cols) {
 #pragma clang fp contract(off)
     // Columns per product chunk (multiple of 16); a chain's row is padded by
-    // four floats so the 16 chains of a lane group read disjoint banks.
-    constexpr uint32_t kStrictChunk = NV == 1 ? 2048 : 512;
+    // four floats so the 16 chains of a lane group read disjoint banks. A
+    // row of up to 2048 columns is one chunk (132 KB of LDS at NV = 16), so
+    // its loads make one round trip before the chains start.
+    constexpr uint32_t kStrictChunk = 2048;
     constexpr uint32_t kPRow = kStrictChunk / 4 + 4;
     __shared__ __align__(16) float P[NV * 4][kPRow];
     const uint32_t r = blockIdx.x, v0 = blockIdx.y * NV;
@@ -305,9 +307,7 @@ __global__ __launch_bounds__(kFloatThreads) void gemv_strict_kernel(const WT* __
     for (uint32_t c0 = 0; c0 < cols4; c0 += kStrictChunk) {
         const uint32_t cn = min(kStrictChunk, cols4 - c0);
         // Product phase: column quad q = c0 / 4 + i, i = tid + 256 k.
-        for (uint32_t i = tid; i < cn / 4; i += kFloatThreads) {
-            const uint32_t col = c0 + 4 * i;
-            float wv[4];
+        auto load_w = [&](uint32_t col, float (&wv)[4]) {
             if constexpr (sizeof(WT) == 2) {
                 const uint2 hv = buf_load_b64(wr, col * 2, 0);
                 wv[0] = f16_bits_to_f32(hv.x & 0xFFFFu);
@@ -321,15 +321,42 @@ __global__ __launch_bounds__(kFloatThreads) void gemv_strict_kernel(const WT* __
                 wv[2] = __uint_as_float(q.z);
                 wv[3] = __uint_as_float(q.w);
             }
+        };
+        auto x_rsrc = [&](int j) {
+            const uint32_t m = v0 + j;
+            return make_rsrc(x + (uint64_t)(m < n_vecs ? m : 0) * x_stride, m < n_vecs ? cols4 * 4 : 0);
+        };
+        auto store = [&](uint32_t i, int j, const float (&wv)[4], const uint4& q) {
+            P[4 * j + 0][i] = wv[0] * __uint_as_float(q.x);
+            P[4 * j + 1][i] = wv[1] * __uint_as_float(q.y);
+            P[4 * j + 2][i] = wv[2] * __uint_as_float(q.z);
+            P[4 * j + 3][i] = wv[3] * __uint_as_float(q.w);
+        };
+        constexpr uint32_t kQpt = kStrictChunk / 4 / kFloatThreads;  // quads per thread in a full chunk
+        if (NV > 1 && cn == kStrictChunk) {
+            // Several vectors, full chunk: every load of the thread's quads
+            // is issued before the first product, one round trip in all.
+            float wv[kQpt][4];
+            uint4 xq[kQpt][NV];
+#pragma unroll
+            for (uint32_t k = 0; k < kQpt; ++k) load_w(c0 + 4 * (tid + kFloatThreads * k), wv[k]);
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
-                const uint32_t m = v0 + j;
-                const BufRsrc xr = make_rsrc(x + (uint64_t)(m < n_vecs ? m : 0) * x_stride, m < n_vecs ? cols4 * 4 : 0);
-                const uint4 q = buf_load_b128(xr, col * 4, 0);
-                P[4 * j + 0][i] = wv[0] * __uint_as_float(q.x);
-                P[4 * j + 1][i] = wv[1] * __uint_as_float(q.y);
-                P[4 * j + 2][i] = wv[2] * __uint_as_float(q.z);
-                P[4 * j + 3][i] = wv[3] * __uint_as_float(q.w);
+                const BufRsrc xr = x_rsrc(j);
+#pragma unroll
+                for (uint32_t k = 0; k < kQpt; ++k) xq[k][j] = buf_load_b128(xr, (c0 + 4 * (tid + kFloatThreads * k)) * 4, 0);
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kQpt; ++k)
+#pragma unroll
+                for (int j = 0; j < NV; ++j) store(tid + kFloatThreads * k, j, wv[k], xq[k][j]);
+        } else {
+            for (uint32_t i = tid; i < cn / 4; i += kFloatThreads) {
+                const uint32_t col = c0 + 4 * i;
+                float wv[4];
+                load_w(col, wv);
+#pragma unroll
+                for (int j = 0; j < NV; ++j) store(i, j, wv, buf_load_b128(x_rsrc(j), col * 4, 0));
             }
         }
         __syncthreads();

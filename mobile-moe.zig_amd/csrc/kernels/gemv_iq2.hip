@@ -265,18 +265,18 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
         RawB raw[2];
         if (p0 < p1) fetch_b(rb[0], tab, mtab, raw[0]);
         for (uint32_t i = p0; i < p1; i += kRing) {
+            // Issue priority by items left, set once per kRing items: the
+            // hardware otherwise favours a SIMD's oldest wave, whose items
+            // then finish far ahead of the youngest's, and the workgroup
+            // waits for the last wave with the CU part idle.
+            const uint32_t rem = p1 - i;
+            if (rem > 8) __builtin_amdgcn_s_setprio(3);
+            else if (rem > 4) __builtin_amdgcn_s_setprio(2);
+            else if (rem > 2) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
 #pragma unroll
             for (int q = 0; q < kRing; ++q) {
                 if (i + q < p1) {
-                    // Issue priority by items left: the hardware otherwise
-                    // favours a SIMD's oldest wave, whose items then finish
-                    // far ahead of the youngest's, and the workgroup waits
-                    // for the last wave with the CU part idle.
-                    const uint32_t rem = p1 - (i + q);
-                    if (rem > 8) __builtin_amdgcn_s_setprio(3);
-                    else if (rem > 4) __builtin_amdgcn_s_setprio(2);
-                    else if (rem > 2) __builtin_amdgcn_s_setprio(1);
-                    else __builtin_amdgcn_s_setprio(0);
                     load(i + q + DEPTH < p1, nxt, rb[(q + DEPTH) % kRing], db[(q + DEPTH) % kRing]);
                     nxt = advance(nxt);
                     if (i + q + 1 < p1) fetch_b(rb[(q + 1) % kRing], tab, mtab, raw[(q + 1) & 1]);

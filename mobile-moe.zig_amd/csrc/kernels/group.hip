@@ -85,14 +85,21 @@ __device__ __forceinline__ void step_group_iq2(const uint4 (&r)[kMaxUnitsPerStep
         const uint32_t ls = iq2_ls_all(r[i], g);
         if (i + 1 < UPS) iq2_decode_unit(r[i + 1], tab, b[nxt]);
         int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+        // Block s's MFMA is issued before block s - 1's products are
+        // weighted, so each MFMA's latency overlaps the previous block's
+        // multiply-adds instead of stalling the wave (the sums are integer:
+        // the order of the adds does not change them).
+        v4i dv[2];
+        dv[0] = mfma_i8(av[0], b[cur][0]);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const v4i dv = mfma_i8(av[s], b[cur][s]);
+            if (s + 1 < 8) dv[(s + 1) & 1] = mfma_i8(av[s + 1], b[cur][s + 1]);
+            const v4i& d = dv[s & 1];
             const int t = (int)(((ls >> (4 * s)) & 15u) * 2 + 1);
-            h0 = __mul24(dv[0], t) + h0;
-            l0 = __mul24(dv[1], t) + l0;
-            h1 = __mul24(dv[2], t) + h1;
-            l1 = __mul24(dv[3], t) + l1;
+            h0 = __mul24(d[0], t) + h0;
+            l0 = __mul24(d[1], t) + l0;
+            h1 = __mul24(d[2], t) + h1;
+            l1 = __mul24(d[3], t) + l1;
             // Keeps each sum a chain of 24-bit multiply-adds (one
             // instruction per product) instead of products plus add trees.
             asm("" : "+v"(h0), "+v"(l0), "+v"(h1), "+v"(l1));
