@@ -67,23 +67,56 @@ __device__ __forceinline__ void lds_a_pair(const uint8_t* aq, uint32_t pair, uin
 // (dequant.zig:336: d * (0.5 + ls) / 4): the eight blocks' digit dot products
 // are weighted by 2 ls + 1 and summed exactly in int32 (24-bit multiplies:
 // |D| <= 32 * 128 * 43, weighted sums < 2^26), then converted and scaled once.
+// B operands of one IQ2_XXS record unit with every LDS read (8 record
+// entries, 8 hi3 mask pairs) issued before the first sign fix, so the unit
+// waits for the table once instead of once per batch of reads; the same
+// values as iq2_decode_unit.
+__device__ __forceinline__ void iq2_decode_unit_batched(const uint4& rr, const uint32_t* tab, long (&b)[8]) {
+    const uint32_t w4[4] = {rr.x, rr.y, rr.z, rr.w};
+    const char* t8 = reinterpret_cast<const char*>(tab);
+    const char* m8 = t8 + kIq2TableWords * 4;
+    uint2 e[8], m[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t d = w4[k];
+        e[2 * k] = *reinterpret_cast<const uint2*>(t8 + (d & 0x7FF8u));
+        m[2 * k] = *reinterpret_cast<const uint2*>(m8 + ((d >> 12) & 0x38u));
+        e[2 * k + 1] = *reinterpret_cast<const uint2*>(t8 + ((d >> 15) & 0x7FF8u));
+        m[2 * k + 1] = *reinterpret_cast<const uint2*>(m8 + ((d << 3) & 0x38u));
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        // (e.y ^ m.x) + m.y as one v_xad_u32 (as plain C the compiler
+        // folds the add into a 64-bit add with the low word: three VALU).
+        uint32_t hi;
+        asm("v_xad_u32 %0, %1, %2, %3" : "=v"(hi) : "v"(e[s].y), "v"(m[s].x), "v"(m[s].y));
+        b[s] = __builtin_bit_cast(long, make_uint2(e[s].x, hi));
+    }
+}
+
 template <int UPS>
 __device__ __forceinline__ void step_group_iq2(const uint4 (&r)[kMaxUnitsPerStep], const uint32_t (&dw)[kMaxUnitsPerStep],
                                                uint32_t ub, const uint8_t* aq, const float* xs0, const float* xs1,
                                                const uint32_t* tab, uint32_t lane, float& acc0, float& acc1) {
     const uint32_t g = lane >> 4;
     long b[2][8];
-    iq2_decode_unit(r[0], tab, b[0]);
+    long av[8];
+    // The first unit's activation reads go out before its table reads, so
+    // both arrive in one LDS round trip.
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lds_a_pair(aq, ub * 4 + q, lane, av[2 * q], av[2 * q + 1]);
+    iq2_decode_unit_batched(r[0], tab, b[0]);
 #pragma unroll
     for (int i = 0; i < UPS; ++i) {
         const int cur = i & 1, nxt = cur ^ 1;
-        long av[8];
+        if (i > 0) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) lds_a_pair(aq, (ub + i) * 4 + q, lane, av[2 * q], av[2 * q + 1]);
+            for (int q = 0; q < 4; ++q) lds_a_pair(aq, (ub + i) * 4 + q, lane, av[2 * q], av[2 * q + 1]);
+        }
         const uint32_t blk0 = (ub + i) * 8;
         const float x0 = xs0[blk0], x1 = xs1[blk0];
         const uint32_t ls = iq2_ls_all(r[i], g);
-        if (i + 1 < UPS) iq2_decode_unit(r[i + 1], tab, b[nxt]);
+        if (i + 1 < UPS) iq2_decode_unit_batched(r[i + 1], tab, b[nxt]);
         int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
         // Block s's MFMA is issued before block s - 1's products are
         // weighted, so each MFMA's latency overlaps the previous block's
