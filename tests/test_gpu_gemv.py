@@ -177,7 +177,7 @@ def test_qmm_batch64_config(ctx, orc, t, rows, cols):
 
 @pytest.mark.parametrize("t", [mm.F32, mm.F16])
 @pytest.mark.parametrize("batch,rows,cols", [(5, 80, 320), (16, 64, 2048), (37, 200, 1024), (64, 64, 2048),
-                                             (9, 48, 330)])
+                                             (9, 48, 330), (17, 40, 4100)])
 def test_float_weights_batched(ctx, orc, t, batch, rows, cols):
     """f32 / f16 weights times a batch (the router of a prefill call,
     batchMatMulUnified's f32 branch: one math.matVecMul per row,
