@@ -256,22 +256,43 @@ def calibration_reads(ctx, n=3, mib=512):
 
 # ---------------------------------------------------------------- headline step
 
-def step_section(ctx, ev, fmt, steps, warmup, pool_gib, rng):
+def step_parity(fmt, raw_gate, raw_down, x_h, xd_h, got_g, got_d, orc):
+    """Every matrix of one headline step against the oracle's
+    matVecMulUnified on the same inputs: the worst max-abs-rel over the 128
+    matrices and the 99.9th percentile of per-element relative error."""
+    pg, pd = mm.tensor_bytes(fmt, INTER, HIDDEN), mm.tensor_bytes(fmt, HIDDEN, INTER)
+    refs, gots = [], []
+    for e in range(EXPERTS):
+        refs.append(orc.mat_vec_mul_unified(raw_gate[e * pg:(e + 1) * pg], fmt, x_h, INTER, HIDDEN))
+        gots.append(got_g[e])
+        refs.append(orc.mat_vec_mul_unified(raw_down[e * pd:(e + 1) * pd], fmt, xd_h[e], HIDDEN, INTER))
+        gots.append(got_d[e])
+    worst = max(mm.max_abs_rel(gv, rv) for gv, rv in zip(gots, refs))
+    p = parity(np.concatenate(gots), np.concatenate(refs))
+    return {"max_abs_rel": float(f"{worst:.3e}"), "p999_rel": p["p999_rel"], "matrices": 2 * EXPERTS,
+            "checked": "one step's outputs after the timed pass, every matrix against the oracle (bar 1e-3)"}
+
+
+def step_section(ctx, ev, fmt, steps, warmup, pool_gib, rng, orc=None):
     """64 matrices of each shape per step in ONE launch (mmhip_gemv_grouped_dev:
     gate/up-shaped [1536 x 2048] with a shared x, down-shaped [2048 x 1536] with
     one x each). The timed pass is bracketed by HIP events on the library's
     stream and by host synchronisations: the kernel time per step and the
     wall time per step come from the same pass. For comparison, the two
-    shapes as separate launches, timed in blocks of back-to-back launches."""
+    shapes as separate launches, timed in blocks of back-to-back launches.
+    With the oracle, one step's outputs are then checked matrix by matrix."""
     raw_gate = mm.make_weight(rng, fmt, INTER, HIDDEN, EXPERTS)
     raw_down = mm.make_weight(rng, fmt, HIDDEN, INTER, EXPERTS)
     per_set = mm.tensor_bytes(fmt, INTER, HIDDEN, EXPERTS) + mm.tensor_bytes(fmt, HIDDEN, INTER, EXPERTS)
     n_sets = max(2, int(pool_gib * GIB // per_set))
     sets = [(ctx.upload(raw_gate, fmt, INTER, HIDDEN, EXPERTS), ctx.upload(raw_down, fmt, HIDDEN, INTER, EXPERTS))
             for _ in range(n_sets)]
-    del raw_gate, raw_down
-    x = mm.DeviceArray.from_numpy(ctx, rng.standard_normal(HIDDEN).astype(np.float32))
-    xd = mm.DeviceArray.from_numpy(ctx, rng.standard_normal((EXPERTS, INTER)).astype(np.float32))
+    if orc is None:
+        del raw_gate, raw_down
+    x_h = rng.standard_normal(HIDDEN).astype(np.float32)
+    xd_h = rng.standard_normal((EXPERTS, INTER)).astype(np.float32)
+    x = mm.DeviceArray.from_numpy(ctx, x_h)
+    xd = mm.DeviceArray.from_numpy(ctx, xd_h)
     yg = mm.DeviceArray(ctx, EXPERTS * INTER * 4)
     yd = mm.DeviceArray(ctx, EXPERTS * HIDDEN * 4)
     groups = [ctx.gemv_groups([(g, 0, EXPERTS, x, 0, yg, INTER), (d, 0, EXPERTS, xd, INTER, yd, HIDDEN)])
@@ -310,6 +331,15 @@ def step_section(ctx, ev, fmt, steps, warmup, pool_gib, rng):
     reps = max(10, steps // 4)
     sep = {"gate_1536x2048_us": round(ev.per_call_us(st, gate, reps), 3),
            "down_2048x1536_us": round(ev.per_call_us(st, down, reps), 3)}
+    step_par = None
+    if orc is not None:
+        yg.zero()
+        yd.zero()
+        step(0)
+        ctx.synchronize()
+        got_g = yg.to_numpy(np.float32, EXPERTS * INTER).reshape(EXPERTS, INTER)
+        got_d = yd.to_numpy(np.float32, EXPERTS * HIDDEN).reshape(EXPERTS, HIDDEN)
+        step_par = step_parity(fmt, raw_gate, raw_down, x_h, xd_h, got_g, got_d, orc)
     for g, d in sets:
         g.free()
         d.free()
@@ -317,7 +347,7 @@ def step_section(ctx, ev, fmt, steps, warmup, pool_gib, rng):
         arr.free()
     return {"step_bytes": b_gate + b_down, "b_gate": b_gate, "b_down": b_down, "dt": dt, "n_sets": n_sets,
             "pool_gib": n_sets * per_set / GIB, "device_us_per_step": device_us, "separate_launches": sep,
-            "first_20_steps_us": first_us, "settle_steps": settle_steps}
+            "first_20_steps_us": first_us, "settle_steps": settle_steps, "parity": step_par}
 
 
 def read_traffic():
@@ -796,7 +826,7 @@ def main():
             res = stream_section(ctx, ev)
         elif only in ("step", "q8step"):
             fmt = mm.IQ2_XXS if only == "step" else mm.Q8_0
-            g = step_section(ctx, ev, fmt, args.steps, args.warmup, args.pool_gib, rng)
+            g = step_section(ctx, ev, fmt, args.steps, args.warmup, args.pool_gib, rng, orc)
             res = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()}
         elif only == "cfg0":
             res = gemv_cfg(ctx, ev, rng, mm.Q8_0, INTER, HIDDEN, args.pool_gib, None, orc, reps)
@@ -824,12 +854,13 @@ def main():
 
     stream = stream_section(ctx, ev)
     sgbs = stream["read_GB/s"]
-    g = step_section(ctx, ev, mm.IQ2_XXS, args.steps, args.warmup, args.pool_gib, rng)
+    g = step_section(ctx, ev, mm.IQ2_XXS, args.steps, args.warmup, args.pool_gib, rng, orc)
     value = g["step_bytes"] * args.steps / g["dt"] / 1e9
     kernel_us = g["device_us_per_step"]
     achieved = g["step_bytes"] / (kernel_us * 1e-6) / 1e9
     traffic = read_traffic()
-    q8 = step_section(ctx, ev, mm.Q8_0, max(20, args.steps // 4), max(5, args.warmup // 4), args.pool_gib, rng)
+    q8 = step_section(ctx, ev, mm.Q8_0, max(20, args.steps // 4), max(5, args.warmup // 4), args.pool_gib, rng,
+                      orc)
     q8_steps = max(20, args.steps // 4)
 
     configs = {
@@ -872,6 +903,7 @@ def main():
             "hidden": HIDDEN, "expert_inter": INTER, "experts_per_launch": EXPERTS,
             "bytes_per_step": g["step_bytes"],
         },
+        "parity": g["parity"],
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -897,6 +929,7 @@ def main():
                     "achieved": round(q8["step_bytes"] / (q8["device_us_per_step"] * 1e-6) / 1e9, 1),
                     "frac": round(q8["step_bytes"] / (q8["device_us_per_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                     "separate_launches": q8["separate_launches"],
+                    "parity": q8["parity"],
                     "workload": "the headline step with Q8_0 weights (64 + 64 matrices, one launch)"},
         "host": host_info(),
     }

@@ -75,7 +75,11 @@ const char* mmhip_version(void);
 int mmhip_init(mmhip_ctx** out_ctx, int device);
 /* OpenCLBackend.deinit (283-300): frees every resident weight. */
 void mmhip_destroy(mmhip_ctx* ctx);
-/* Wait for all work queued on the context's stream (clFinish). */
+/* Wait for all work queued on the context's stream (clFinish). Also reports
+ * a failed grid-wide wait of an earlier one-launch MoE decode
+ * (mmhip_moe_ffn_dev): MMHIP_ERR_HIP with the reason, once, and the status
+ * is cleared. A caller that synchronises the raw stream from mmhip_stream()
+ * instead never sees that error. */
 int mmhip_synchronize(mmhip_ctx* ctx);
 /* The context's hipStream_t, as an opaque pointer. */
 void* mmhip_stream(mmhip_ctx* ctx);
@@ -345,11 +349,27 @@ void mmhip_moe_layer_destroy(mmhip_ctx* ctx, mmhip_moe_layer* layer);
 /* n_tokens hidden vectors in, n_tokens FFN outputs out (host buffers,
  * synchronous). route_ids / route_weights (optional, [n_tokens][4]) receive
  * Scheduler.route's expert_ids / weights; unused slots hold 0xFFFFFFFF / 0.
- * Returns k (experts per token) or < 0. */
+ * Returns k (experts per token) or < 0.
+ *
+ * One-token calls on a layer with IQ2_XXS experts (shared expert merged or
+ * absent) run as ONE launch whose workgroups (one per CU) hand work to each
+ * other, so all of them must be resident at once. That holds while no other
+ * kernel occupies the device's CUs (another stream, context or process);
+ * one that does delays the launch until its CUs free up. A hand-over wait
+ * that is not satisfied within 10 ms (MMHIP_DECODE_WAIT_US) gives up: the
+ * launch still ends, its output is invalid, and the error is returned by
+ * this call, or, for mmhip_moe_ffn_dev, by the next mmhip_synchronize or
+ * mmhip_moe_ffn on the context. MMHIP_DECODE_FUSED=0 (read at layer
+ * creation) selects three ordinary launches, which need no residency, and
+ * MMHIP_DECODE_COOP=1 a cooperative launch, which guarantees it (~18 us
+ * more per call). */
 int mmhip_moe_ffn(mmhip_ctx* ctx, mmhip_moe_layer* layer, const float* hidden_host,
                   float* out_host, uint32_t n_tokens, const mmhip_route_params* rp,
                   uint32_t* route_ids_host, float* route_weights_host);
-/* Device twin (asynchronous). route_*_dev may be NULL. Returns 0 or < 0. */
+/* Device twin (asynchronous). route_*_dev may be NULL. Returns 0 or < 0;
+ * a failed hand-over wait of its one-launch decode (above) is reported by
+ * the next mmhip_synchronize or mmhip_moe_ffn, after work queued behind it
+ * may already have read the invalid output. */
 int mmhip_moe_ffn_dev(mmhip_ctx* ctx, mmhip_moe_layer* layer, const float* hidden_dev,
                       float* out_dev, uint32_t n_tokens, const mmhip_route_params* rp,
                       uint32_t* route_ids_dev, float* route_weights_dev);

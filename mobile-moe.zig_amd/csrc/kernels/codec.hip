@@ -276,12 +276,20 @@ struct RowBlock {
     uint32_t blk;
 };
 __device__ __forceinline__ RowBlock row_block(uint64_t row0, uint32_t blk0, uint32_t k, uint32_t bpr, float inv_bpr) {
-    // 24-bit multiplies (full rate): t < 2^24 and bpr < 2^24 here.
+    // t < bpr + 2^10 < 2^28 (row_len < 2^32), so q * bpr <= t + bpr fits in
+    // 32 bits. 24-bit multiplies (full rate) need both factors below 2^24,
+    // which holds for q always and for bpr on rows of fewer than 2^29
+    // values; longer rows take the 32-bit multiplies (the branch is uniform).
     const uint32_t t = blk0 + k;
     uint32_t q = (uint32_t)((float)t * inv_bpr);
-    if (__umul24(q, bpr) > t) --q;
-    if (__umul24(q + 1, bpr) <= t) ++q;
-    return RowBlock{row0 + q, t - __umul24(q, bpr)};
+    if (bpr < (1u << 24)) {
+        if (__umul24(q, bpr) > t) --q;
+        if (__umul24(q + 1, bpr) <= t) ++q;
+        return RowBlock{row0 + q, t - __umul24(q, bpr)};
+    }
+    if (q * bpr > t) --q;
+    if ((q + 1) * bpr <= t) ++q;
+    return RowBlock{row0 + q, t - q * bpr};
 }
 
 __global__ __launch_bounds__(kQ8Threads) void quantize_q8_0_rows_kernel(const float* __restrict__ x,

@@ -2,8 +2,8 @@
 // token (inference.zig:886-1010) with the router matVecMul (math.zig:79-99,
 // called at inference.zig:903), Scheduler.route (scheduler.zig:169-262),
 // expertFFN (inference.zig:1152-1188) over the routed experts and the merged
-// shared expert, and the weighted combine, in a single cooperative launch of
-// one 1024-thread workgroup per CU.
+// shared expert, and the weighted combine, in a single launch of one
+// 1024-thread workgroup per CU.
 //
 // At one token the layer is a chain of short dependent steps (router scores ->
 // routing -> gate/up -> down -> sum), each moving a few MB: as separate
@@ -42,16 +42,16 @@
 //   - an h block is written with device-scope stores; once they are performed
 //     (s_waitcnt vmcnt(0)), its flag word is set to the epoch. Consumers poll
 //     the flags with device-scope loads and then read the blocks' digit
-//     planes with plain loads, which the XCD's L2 shares between its
-//     workgroups: nothing in the launch reads a plane line before every
-//     block on it is published, and lines cached by earlier launches are
-//     invalidated at the launch boundary. The block scales (several
-//     problems' to a line) are read with device-scope loads.
+//     planes and scales with device-scope loads too, so no line another
+//     XCD wrote is served stale from this XCD's L2.
 // The memory model's agent-scope release/acquire fences write back and
 // invalidate the whole L2 per use, and a single shared counter serialises
 // hundreds of atomics; both cost several microseconds per hand-over here.
-// A wait gives up after a bounded spin and records the failure in a host-
-// visible status word, so a launch always ends.
+// A plain launch needs every workgroup resident at once (one per CU), which
+// holds on a device no other kernel occupies; a launch that cannot become
+// resident fails instead of hanging: a wait gives up after a bounded time
+// and records the failure in a host-visible status word, so a launch
+// always ends.
 #include "iq2_ops.hpp"
 #include "kernels.hpp"
 #include "route_ops.hpp"
@@ -103,14 +103,17 @@ __device__ __forceinline__ void publish_u32(uint32_t* p, uint32_t v) {
 // into v, done(v) tells whether everything it read is published. One round
 // is in flight at a time: a second one issued ahead would still be in
 // flight on return, and the next use of its registers would wait for it.
-// After 1 + limit rounds the wait gives up and records `code`.
+// The wait is bounded by time, read from the constant 100 MHz real-time
+// counter (s_memrealtime, 10 ns per tick): once `ticks` have passed since
+// the first poll (0: after the first poll), it gives up and records `code`.
 template <typename V, typename Load, typename Done>
-__device__ __forceinline__ void grid_wait(V& v, Load load, Done done, uint32_t limit, uint32_t* status,
+__device__ __forceinline__ void grid_wait(V& v, Load load, Done done, uint32_t ticks, uint32_t* status,
                                           uint32_t code) {
-    for (uint32_t spins = 0;; ++spins) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
         load(v);
         if (done(v)) return;
-        if (spins >= limit) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) {
             if (status) __hip_atomic_store(status, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             return;
         }
@@ -389,7 +392,7 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
                 for (int q = 0; q < 4; ++q) ok = ok && (uint32_t)(t.v[q] >> 32) == epoch;
                 return __all(ok) != 0;
             },
-            a.spin_limit, a.status, 1u);
+            a.wait_ticks, a.status, 1u);
         float sc[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) sc[q] = __uint_as_float((uint32_t)ta.v[q]);
@@ -469,14 +472,12 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
         auto stage = [&](uint32_t j0, uint32_t j1) {
             // Jobs [j0, j1) (whole problems): wait for their flags (wave 0),
             // copy their h planes and scales into LDS, then the down items of
-            // their problems. The planes are read with plain loads: they are
-            // published, each problem's planes fill whole 128-byte lines
-            // (nbh * 64 bytes), and no line of them was cached before. The
-            // scales are read with device-scope loads: one line holds several
-            // problems' scales, so a plain load of some problems' scales
-            // could cache a line that other problems' scales are later
-            // written to (a first stage over the shared expert's blocks,
-            // measured slower, did exactly that).
+            // their problems. Planes and scales are read with device-scope
+            // loads, which miss in this XCD's L2 for lines another XCD
+            // wrote: the flag loads above are relaxed, so nothing else
+            // orders a plain load after the writer's stores, and a line
+            // cached before them (a scale line holds several problems'
+            // scales) would be stale.
             if (wave == 0) {
                 constexpr int kQ = (kDmMaxHBlocks + 63) / 64;  // flags per lane, at most
                 struct Flags {
@@ -499,12 +500,12 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
                         for (int q = 0; q < kQ; ++q) ok = ok && f.v[q] == epoch;
                         return __all(ok) != 0;
                     },
-                    a.spin_limit, a.status, 2u);
+                    a.wait_ticks, a.status, 2u);
             }
             lds_barrier();
             const BufRsrc qr = make_rsrc(a.hq + (uint64_t)j0 * 64, (j1 - j0) * 64);
             for (uint32_t o = threadIdx.x * 16; o < (j1 - j0) * 64; o += kDmWg * 16)
-                *reinterpret_cast<uint4*>(lds.hq + j0 * 64 + o) = buf_load_b128(qr, o, 0);
+                *reinterpret_cast<uint4*>(lds.hq + j0 * 64 + o) = buf_load_b128<kCacheDevice>(qr, o, 0);
             const BufRsrc sr = make_rsrc(a.hs + j0, (j1 - j0) * 4);
             if (threadIdx.x < j1 - j0)
                 lds.hs[j0 + threadIdx.x] = __uint_as_float(buf_load_b32<kCacheDevice>(sr, threadIdx.x * 4, 0));

@@ -192,13 +192,15 @@ struct DecodeMoeArgs {
     uint64_t* score_tags;       // [n_experts] (epoch << 32 | score bits), published by the router rows
     uint32_t* h_flags;          // [5][inter / 32] epoch of the call whose h block is published
     uint32_t epoch;             // this call's number, never 0; the buffers above start zeroed
-    uint32_t spin_limit;        // polls after the first before a grid wait gives up
+    uint32_t wait_ticks;        // 10 ns ticks after its first poll before a grid wait gives up
     uint32_t* status;           // host-visible word: nonzero when a grid wait timed out
     const float* bias;          // deferral bias [hidden] or null
     float* out;                 // [hidden]
 };
 bool decode_moe_iq2_fits(uint32_t hidden, uint32_t inter, uint32_t n_experts, int num_cu);
-constexpr uint32_t kDecodeSpinLimit = 1u << 22;  // ~2 s of polls: far beyond any launch that can finish
+// Default bound of one grid-wide wait: 10 ms, far beyond a launch whose
+// workgroups are all resident (its waits take microseconds).
+constexpr uint32_t kDecodeWaitUs = 10000;
 hipError_t launch_decode_moe_iq2(const DecodeMoeArgs& a, int num_cu, hipStream_t s);
 
 // Allocation-free QMM scratch (noalloc.hip): kNoallocScratchBytes of device

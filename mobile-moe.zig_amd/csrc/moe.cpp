@@ -81,7 +81,7 @@ struct mmhip_moe_layer {
     uint32_t* dm_flags = nullptr;   // [5][inter / 32] epoch-tagged h blocks
     uint32_t dm_epoch = 0;          // number of the last one-launch call (never 0 once called)
     bool decode_fused = false;  // the layer's decode calls use the one-launch kernel
-    uint32_t dm_spin_limit = 0;  // polls before a grid-wide wait gives up
+    uint32_t dm_wait_ticks = 0;  // 10 ns ticks before a grid-wide wait gives up
     float* d_in = nullptr;   // host-ABI staging [T][hidden]
     float* d_out = nullptr;
 };
@@ -284,7 +284,7 @@ int ffn_enqueue(mmhip_ctx* ctx, mmhip_moe_layer* L, const float* hidden, float* 
         d.h_flags = L->dm_flags;
         if (++L->dm_epoch == 0) L->dm_epoch = 1;
         d.epoch = L->dm_epoch;
-        d.spin_limit = L->dm_spin_limit;
+        d.wait_ticks = L->dm_wait_ticks;
         d.status = ctx->status_dev;
         d.bias = with_bias ? L->bias : nullptr;
         d.out = out;
@@ -500,11 +500,12 @@ int mmhip_moe_layer_create(mmhip_ctx* ctx, const mmhip_moe_weights* wts, mmhip_m
     L->decode_fused = !(fused_env && fused_env[0] == '0') && L->gu->geom.fmt == kFmtIq2 &&
                       L->dn->geom.fmt == kFmtIq2 && (!has_shared || L->shared_merged) &&
                       decode_moe_iq2_fits(L->hidden, L->inter, L->n_experts, ctx->num_cu);
-    // MMHIP_DECODE_SPIN_LIMIT=n: a grid-wide wait gives up after 1 + n polls
-    // and the call reports an error (tests force the failure path with 0).
-    const char* spin_env = getenv("MMHIP_DECODE_SPIN_LIMIT");
-    const unsigned long spin = spin_env ? strtoul(spin_env, nullptr, 10) : kDecodeSpinLimit;
-    L->dm_spin_limit = (uint32_t)(spin < (1ul << 26) ? spin : (1ul << 26));
+    // MMHIP_DECODE_WAIT_US=n: a grid-wide wait gives up n microseconds after
+    // its first poll (0: after the first poll) and the call reports an error
+    // (tests force the failure path with 0). At most 40 s.
+    const char* wait_env = getenv("MMHIP_DECODE_WAIT_US");
+    const unsigned long wait_us = wait_env ? strtoul(wait_env, nullptr, 10) : kDecodeWaitUs;
+    L->dm_wait_ticks = (uint32_t)(wait_us < 40000000ul ? wait_us : 40000000ul) * 100u;  // 100 MHz ticks
     *out_layer = L;
     return MMHIP_OK;
 }

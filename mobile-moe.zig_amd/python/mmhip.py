@@ -544,6 +544,7 @@ class MoeLayer:
         h = _c_void_p()
         check(ctx.lib.mmhip_moe_layer_create(ctx.handle, ctypes.byref(w), ctypes.byref(h)), "mmhip_moe_layer_create")
         self.handle = h.value
+        self._plan = None  # the PlanDispatch this layer is bound to, if any
 
     @classmethod
     def from_gguf(cls, ctx: Context, g: "Gguf", layer: int) -> "MoeLayer":
@@ -558,6 +559,7 @@ class MoeLayer:
         check(ctx.lib.mmhip_moe_layer_create_gguf(ctx.handle, g.handle, layer, ctypes.byref(h)),
               "mmhip_moe_layer_create_gguf")
         self.handle = h.value
+        self._plan = None
         return self
 
     def free(self):
@@ -575,6 +577,16 @@ class MoeLayer:
 
     def ffn(self, hidden: np.ndarray, level: int = 0, active_expert_limit: int = 0,
             deferral_bias: Optional[np.ndarray] = None):
+        """moeFFN for the tokens in `hidden`. A layer bound to a PlanDispatch
+        runs only through it: a direct call raises MmhipError (ERR_INVALID),
+        so no layer's routed experts run twice for one token."""
+        if self._plan is not None:
+            raise MmhipError("moe_ffn", ERR_INVALID,
+                             "the layer is bound to a PlanDispatch; its FFN runs at the plan's ffn_gate_up")
+        return self._ffn(hidden, level, active_expert_limit, deferral_bias)
+
+    def _ffn(self, hidden: np.ndarray, level: int = 0, active_expert_limit: int = 0,
+             deferral_bias: Optional[np.ndarray] = None):
         hidden = np.ascontiguousarray(hidden, dtype=np.float32).reshape(-1, self.hidden)
         t = hidden.shape[0]
         out = np.empty_like(hidden)
@@ -586,6 +598,9 @@ class MoeLayer:
         return out, ids[:, :k], wts[:, :k]
 
     def ffn_dev(self, hidden: DeviceArray, out: DeviceArray, n_tokens: int, rp: Optional[RouteParams] = None):
+        if self._plan is not None:
+            raise MmhipError("moe_ffn_dev", ERR_INVALID,
+                             "the layer is bound to a PlanDispatch; its FFN runs at the plan's ffn_gate_up")
         rp = rp if rp is not None else self.route_params()
         check(self.ctx.lib.mmhip_moe_ffn_dev(self.ctx.handle, self.handle, hidden.ptr, out.ptr, n_tokens,
                                              ctypes.byref(rp), None, None), "mmhip_moe_ffn_dev")
@@ -655,17 +670,36 @@ class PlanDispatch:
     inside it, and ffn_down hands the result back (hidden <- ffn_out,
     inference.zig:1009). Other ops raise MmhipError with ERR_UNSUPPORTED (the
     executor keeps them on its CPU path); siluMul or ffn_down without a
-    preceding ffn_gate_up raise it with ERR_INVALID."""
+    preceding ffn_gate_up raise it with ERR_INVALID.
+
+    The reference's plan for a MoE layer names only the shared expert's
+    gate/up, siluMul and down (scheduler.zig:466-501) and leaves the routed
+    experts to moeFFN; here the plan's FFN ops carry the whole layer. A layer
+    therefore runs through exactly one of the two paths: binding it to a
+    PlanDispatch makes its direct ffn / ffn_dev calls (moeFFN's path) raise
+    ERR_INVALID until release(), and a layer binds to one PlanDispatch at a
+    time."""
 
     def __init__(self, moe: Optional["MoeLayer"], level: int = 0):
+        if moe is not None and moe._plan is not None:
+            raise MmhipError("plan dispatch", ERR_INVALID, "the MoE layer is already bound to a PlanDispatch")
         self.moe, self.level = moe, level
+        self.ffn_out = None
+        if moe is not None:
+            moe._plan = self
+
+    def release(self) -> None:
+        """Unbinds the layer: moeFFN's direct calls work again."""
+        if self.moe is not None and self.moe._plan is self:
+            self.moe._plan = None
+        self.moe = None
         self.ffn_out = None
 
     def dispatch_gpu(self, op: OpSchedule, hidden: np.ndarray) -> None:
         if op.op == OP["ffn_gate_up"]:
             if self.moe is None:
                 raise MmhipError("plan dispatch", ERR_UNSUPPORTED, "no MoE layer for ffn_gate_up")
-            self.ffn_out = self.moe.ffn(hidden, level=self.level)[0].reshape(hidden.shape)
+            self.ffn_out = self.moe._ffn(hidden, level=self.level)[0].reshape(hidden.shape)
         elif op.op == OP["siluMul"]:
             if self.ffn_out is None:
                 raise MmhipError("plan dispatch", ERR_INVALID, "siluMul before ffn_gate_up")

@@ -315,6 +315,10 @@ pub const MoeLayer = struct {
     backend: *HipBackend,
     handle: *MoeLayerHandle,
     hidden: u32,
+    /// Set while a PlanDispatch owns the layer (PlanDispatch.bind): the
+    /// plan's FFN ops then run the whole moeFFN, and a direct ffn call
+    /// returns error.HipInvalidArgument, so no token's experts run twice.
+    plan_bound: bool = false,
 
     /// Uploads one layer's router, routed experts and shared expert.
     pub fn create(backend: *HipBackend, w: MoeWeights) !MoeLayer {
@@ -339,6 +343,11 @@ pub const MoeLayer = struct {
     /// moeFFN for n tokens (hidden / out: [n][hidden]); route ids and weights
     /// ([n][4]) as Scheduler.route returns them. Returns k.
     pub fn ffn(self: *MoeLayer, hidden: []const f32, out: []f32, n_tokens: u32, rp: RouteParams, route_ids: ?[]u32, route_weights: ?[]f32) !u32 {
+        if (self.plan_bound) return error.HipInvalidArgument;
+        return self.ffnUnbound(hidden, out, n_tokens, rp, route_ids, route_weights);
+    }
+
+    fn ffnUnbound(self: *MoeLayer, hidden: []const f32, out: []f32, n_tokens: u32, rp: RouteParams, route_ids: ?[]u32, route_weights: ?[]f32) !u32 {
         std.debug.assert(n_tokens >= 1 and n_tokens <= max_moe_tokens);
         std.debug.assert(hidden.len >= n_tokens * self.hidden and out.len >= n_tokens * self.hidden);
         const rc = mmhip_moe_ffn(self.backend.ctx, self.handle, hidden.ptr, out.ptr, n_tokens, &rp, if (route_ids) |r| r.ptr else null, if (route_weights) |r| r.ptr else null);
@@ -365,6 +374,12 @@ pub const MoeLayer = struct {
 /// Ops this backend does not run (attention, RMSNorm, RoPE, or a dense
 /// layer's FFN without a MoeLayer) return error.HipUnsupportedType, and the
 /// executor keeps them on its CPU path.
+/// The reference's plan for a MoE layer names only the shared expert's
+/// gate/up, siluMul and down (scheduler.zig:466-501) and leaves the routed
+/// experts to moeFFN; here the plan's FFN ops run the whole layer. A layer
+/// therefore runs through exactly one path: bind() takes it for the plan
+/// (moeFFN's direct MoeLayer.ffn then fails with error.HipInvalidArgument,
+/// and so does a second bind), release() gives it back.
 pub const PlanDispatch = struct {
     moe: ?*MoeLayer,
     /// [hidden_size] buffer owned by the caller: the FFN output between
@@ -373,12 +388,26 @@ pub const PlanDispatch = struct {
     route: RouteParams = .{},
     pending: bool = false,
 
+    pub fn bind(moe: ?*MoeLayer, ffn_out: []f32, route: RouteParams) !PlanDispatch {
+        if (moe) |L| {
+            if (L.plan_bound) return error.HipInvalidArgument;
+            L.plan_bound = true;
+        }
+        return .{ .moe = moe, .ffn_out = ffn_out, .route = route };
+    }
+
+    pub fn release(self: *PlanDispatch) void {
+        if (self.moe) |L| L.plan_bound = false;
+        self.moe = null;
+        self.pending = false;
+    }
+
     pub fn dispatchGpu(self: *PlanDispatch, op: scheduler.OpSchedule, hidden: []f32) !void {
         switch (op.op) {
             .ffn_gate_up => {
                 const L = self.moe orelse return error.HipUnsupportedType;
                 std.debug.assert(hidden.len == L.hidden and self.ffn_out.len == L.hidden);
-                _ = try L.ffn(hidden, self.ffn_out, 1, self.route, null, null);
+                _ = try L.ffnUnbound(hidden, self.ffn_out, 1, self.route, null, null);
                 self.pending = true;
             },
             // SiLU(gate) * up is formed on the device inside the FFN call.

@@ -296,3 +296,22 @@ def test_q8_0_large_random_match_oracle(ctx, orc, scale):
         assert bad.size == 0, f"{bad.size} bytes differ, first at {bad[:6]}"
     finally:
         dx.free(); db.free()
+
+
+def test_q8_0_one_row_past_2_pow_29(ctx, orc):
+    """quantize_q8_0 and dequantize over one row of 2^29 + 32,000 values, so
+    the row holds 2^24 + 1,000 blocks: the row split must not use 24-bit
+    multiplies there (block 2^24 + 999 stays in row 0). Bit-exact against the
+    oracle, including the blocks past 2^24."""
+    n = (1 << 29) + 32000
+    rng = np.random.default_rng(29)
+    x = rng.standard_normal(n, dtype=np.float32)
+    blocks = ctx.quantize_q8_0(x)
+    ref = orc.quantize_q8_0(x)
+    bad = np.nonzero(blocks != ref)[0]
+    assert bad.size == 0, f"{bad.size} bytes differ, first at {bad[:6]}"
+    del x, ref
+    got = ctx.dequantize(blocks, mm.Q8_0, n)
+    want = orc.dequantize(blocks, orc.Q8_0, n)
+    bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
+    assert bad.size == 0, f"{bad.size} values differ, first at {bad[:6]}"

@@ -166,7 +166,7 @@ def test_one_launch_decode_many_experts(ctx, orc, n_exp, shared, router_type):
 
 def test_one_launch_decode_wait_timeout_is_reported(ctx):
     """A grid-wide wait that gives up is reported, not silent: with
-    MMHIP_DECODE_SPIN_LIMIT=0 each wait polls once, so workgroups that reach
+    MMHIP_DECODE_WAIT_US=0 each wait polls once, so workgroups that reach
     the routing before the router rows are published give up (the launch
     still ends). The call returns the HIP error code with the reason, the
     context's status is cleared, and a layer with the default limit then
@@ -176,14 +176,14 @@ def test_one_launch_decode_wait_timeout_is_reported(ctx):
     router, gate, up, down, sh = _weights(rng, H, I, E, True)
     kw = dict(hidden=H, inter=I, n_experts=E, expert_type=mm.IQ2_XXS, router=router, gate=gate, up=up, down=down,
               shared=sh, shared_inter=I, shared_type=mm.IQ2_XXS)
-    prev = os.environ.pop("MMHIP_DECODE_SPIN_LIMIT", None)
-    os.environ["MMHIP_DECODE_SPIN_LIMIT"] = "0"
+    prev = os.environ.pop("MMHIP_DECODE_WAIT_US", None)
+    os.environ["MMHIP_DECODE_WAIT_US"] = "0"
     try:
         hasty = mm.MoeLayer(ctx, **kw)
     finally:
-        os.environ.pop("MMHIP_DECODE_SPIN_LIMIT", None)
+        os.environ.pop("MMHIP_DECODE_WAIT_US", None)
         if prev is not None:
-            os.environ["MMHIP_DECODE_SPIN_LIMIT"] = prev
+            os.environ["MMHIP_DECODE_WAIT_US"] = prev
     fused, split, _ = _pair(ctx, H, I, E, router, gate, up, down, sh)
     try:
         errors = []

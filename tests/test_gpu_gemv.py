@@ -316,3 +316,55 @@ def test_gemv_grouped_rejects_bad_groups(ctx):
     finally:
         for a in (wq, wi, x, y):
             a.free()
+
+
+@pytest.mark.parametrize("t", [mm.IQ2_XXS, mm.Q8_0])
+def test_headline_step_shape_matches_oracle(ctx, orc, t):
+    """The benchmark's headline launch exactly as it is measured: one
+    mmhip_gemv_grouped_dev call over 64 distinct [1536 x 2048] matrices with a
+    shared x and 64 distinct [2048 x 1536] matrices with one x each (the
+    routed experts' gate/up and down of a GLM-4.7-Flash layer,
+    inference.zig:1171-1185). The launcher gives each workgroup 48 (gate
+    shape) or 64 (down shape) row tiles, which fills all of its LDS partial
+    slots. Every matrix against the oracle's matVecMulUnified within 1e-3;
+    IQ2_XXS also bit for bit against one mmhip_gemv_batched_dev launch per
+    matrix."""
+    E, H, I = 64, 2048, 1536
+    rng = np.random.default_rng(4100 + t)
+    raw_g = mm.make_weight(rng, t, I, H, E)
+    raw_d = mm.make_weight(rng, t, H, I, E)
+    x = rng.standard_normal(H).astype(np.float32)
+    xd = rng.standard_normal((E, I)).astype(np.float32)
+    wg, wd = ctx.upload(raw_g, t, I, H, E), ctx.upload(raw_d, t, H, I, E)
+    dx, dxd = mm.DeviceArray.from_numpy(ctx, x), mm.DeviceArray.from_numpy(ctx, xd)
+    yg, yd = mm.DeviceArray(ctx, E * I * 4), mm.DeviceArray(ctx, E * H * 4)
+    yg1, yd1 = mm.DeviceArray(ctx, I * 4), mm.DeviceArray(ctx, H * 4)
+    try:
+        ctx.gemv_grouped_dev([(wg, 0, E, dx, 0, yg, I), (wd, 0, E, dxd, I, yd, H)])
+        ctx.synchronize()
+        got_g = yg.to_numpy(np.float32, E * I).reshape(E, I)
+        got_d = yd.to_numpy(np.float32, E * H).reshape(E, H)
+        pg, pd = mm.tensor_bytes(t, I, H), mm.tensor_bytes(t, H, I)
+        worst = 0.0
+        for e in range(E):
+            rg = orc.mat_vec_mul_unified(raw_g[e * pg:(e + 1) * pg], t, x, I, H)
+            rd = orc.mat_vec_mul_unified(raw_d[e * pd:(e + 1) * pd], t, xd[e], H, I)
+            worst = max(worst, mm.max_abs_rel(got_g[e], rg), mm.max_abs_rel(got_d[e], rd))
+        assert worst <= TOL_GEMV, worst
+        if t == mm.IQ2_XXS:
+            for e in (0, 1, 17, 40, 63):
+                ctx.gemv_batched_dev(wg, e, 1, dx, 0, yg1, 0)
+                ctx.synchronize()
+                _bits_equal(got_g[e], yg1.to_numpy(np.float32, I))
+            # Down shape: each single-matrix launch takes its own x row.
+            for e in (0, 5, 63):
+                xe = mm.DeviceArray.from_numpy(ctx, np.ascontiguousarray(xd[e]))
+                try:
+                    ctx.gemv_batched_dev(wd, e, 1, xe, 0, yd1, 0)
+                    ctx.synchronize()
+                    _bits_equal(got_d[e], yd1.to_numpy(np.float32, H))
+                finally:
+                    xe.free()
+    finally:
+        for a in (wg, wd, dx, dxd, yg, yd, yg1, yd1):
+            a.free()

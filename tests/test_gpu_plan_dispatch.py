@@ -51,21 +51,54 @@ def test_gpu_ops_of_a_moe_layer_plan(layer, seed):
     rng = np.random.default_rng(100 + seed)
     x = rng.standard_normal(H).astype(np.float32)
     hidden = x.copy()
-    ran = execute(plan, mm.PlanDispatch(gpu), hidden)
+    d = mm.PlanDispatch(gpu)
+    try:
+        ran = execute(plan, d, hidden)
+    finally:
+        d.release()
     assert ran == [mm.OP["ffn_gate_up"], mm.OP["siluMul"], mm.OP["ffn_down"]]
     ref = cpu.ffn(x[None, :])[0].reshape(-1)
     assert mm.max_abs_rel(hidden, ref) <= 1e-3
+
+
+def test_a_layer_runs_through_one_path(layer):
+    """The reference plans only the shared expert for a MoE layer and leaves
+    the routed experts to moeFFN (scheduler.zig:466-501); here the plan's FFN
+    ops run the whole layer, so a layer bound to a PlanDispatch refuses
+    moeFFN's direct call (and a second binding) until it is released, and no
+    token's routed experts run twice."""
+    gpu, cpu = layer
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(H).astype(np.float32)
+    d = mm.PlanDispatch(gpu)
+    try:
+        with pytest.raises(mm.MmhipError) as e:
+            gpu.ffn(x[None, :])
+        assert e.value.code == mm.ERR_INVALID
+        with pytest.raises(mm.MmhipError) as e:
+            mm.PlanDispatch(gpu)
+        assert e.value.code == mm.ERR_INVALID
+        hidden = x.copy()
+        execute(mm.plan_layer(3, has_gpu=True, **HP), d, hidden)
+    finally:
+        d.release()
+    direct = gpu.ffn(x[None, :])[0].reshape(-1)
+    np.testing.assert_array_equal(direct.view(np.uint32), hidden.view(np.uint32))
+    assert mm.max_abs_rel(direct, cpu.ffn(x[None, :])[0].reshape(-1)) <= 1e-3
 
 
 def test_dispatch_errors(layer):
     gpu, _ = layer
     d = mm.PlanDispatch(gpu)
     h = np.zeros(H, np.float32)
-    for name, code in (("siluMul", mm.ERR_INVALID), ("ffn_down", mm.ERR_INVALID), ("attention", mm.ERR_UNSUPPORTED),
-                       ("rmsNorm", mm.ERR_UNSUPPORTED)):
-        with pytest.raises(mm.MmhipError) as e:
-            d.dispatch_gpu(mm.op_schedule(mm.OP[name], mm.BACKEND_GPU, 0, 0, False), h)
-        assert e.value.code == code
+    try:
+        for name, code in (("siluMul", mm.ERR_INVALID), ("ffn_down", mm.ERR_INVALID),
+                           ("attention", mm.ERR_UNSUPPORTED), ("rmsNorm", mm.ERR_UNSUPPORTED)):
+            with pytest.raises(mm.MmhipError) as e:
+                d.dispatch_gpu(mm.op_schedule(mm.OP[name], mm.BACKEND_GPU, 0, 0, False), h)
+            assert e.value.code == code
+    finally:
+        d.release()
     # A dense layer (no MoeLayer) keeps its FFN on the CPU path.
     with pytest.raises(mm.MmhipError) as e:
         mm.PlanDispatch(None).dispatch_gpu(mm.op_schedule(mm.OP["ffn_gate_up"], mm.BACKEND_GPU, 0, 0, False), h)
