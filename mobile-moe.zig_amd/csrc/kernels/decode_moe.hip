@@ -10,8 +10,9 @@
 // launches every step pays a launch ramp, a first-load latency and a drain.
 // Here the steps hand over inside the launch:
 //
-//   1. The last E workgroups compute one router row each in math.matVecMul's
-//      summation order (as gemv_strict_kernel does) and publish the score.
+//   1. E workgroups (the first ones without a shared-expert job) compute one
+//      router row each in math.matVecMul's summation order (as
+//      gemv_strict_kernel does) and publish the score.
 //      Meanwhile every workgroup loads the IQ2_XXS tables and quantises the
 //      hidden vector into LDS, and the shared expert's gate/up jobs (which do
 //      not depend on the routing) are computed.
@@ -208,13 +209,16 @@ __global__ __launch_bounds__(kDmWg, 1) void decode_moe_iq2_kernel(DecodeMoeArgs 
     const uint32_t sh = a.route.shared ? 1u : 0u;  // problem 0 is the shared expert when present
 
     // ---- Router row loads first (the routing waits on them): row r on
-    // workgroup G - E + r, the last workgroups, which have no shared-expert
-    // job (vector loads return in issue order, so a job's weight loads would
-    // hold the row's loads back). Other workgroups' resources are empty (the
-    // loads read zeros without a memory access), so every load is issued
-    // unconditionally and the compiler's load counters stay exact.
-    const bool router_wg = w >= G - E;
-    const uint32_t r_row = router_wg ? w - (G - E) : 0;
+    // workgroup r0 + r, the first workgroups without a shared-expert job
+    // (vector loads return in issue order, so a job's weight loads would
+    // hold the row's loads back). Workgroups are dispatched in id order, so
+    // low ids start earliest: 0.3 us per token sooner than on the last E.
+    // Other workgroups' resources are empty (the loads read zeros without a
+    // memory access), so every load is issued unconditionally and the
+    // compiler's load counters stay exact.
+    const uint32_t r0 = G >= sh * nbh + E ? sh * nbh : G - E;
+    const bool router_wg = w >= r0 && w < r0 + E;
+    const uint32_t r_row = router_wg ? w - r0 : 0;
     const bool f16_router = a.router_type != 0;
     const uint32_t rbytes = router_wg ? a.hidden * (f16_router ? 2u : 4u) : 0u;
     const char* rrow = static_cast<const char*>(a.router_w) + (uint64_t)r_row * a.hidden * (f16_router ? 2u : 4u);
