@@ -419,7 +419,9 @@ def qmm_cfg(ctx, ev, rng, rows, cols, batch, pool_gib, stream_gbs, orc, reps):
     out = {"shape": f"X[{batch} x {cols}] . W[{rows} x {cols}]^T", "bytes": nbytes, **rate(nbytes, us, stream_gbs),
            "TFLOP/s": round(flop / (us * 1e-6) / 1e12, 2), "flop": flop, "copies": n,
            "pool_MiB": round(n * mm.tensor_bytes(fmt, rows, cols) / (1 << 20)),
-           "launches_per_call": 2, "note": "two launches per call: activation quantisation, then the int8-digit MFMA"}
+           "launches_per_call": 1 if cols <= 2048 else 2,
+           "note": ("one launch per call: the activations are quantised inside the int8-digit MFMA kernel"
+                    if cols <= 2048 else "two launches per call: activation quantisation, then the int8-digit MFMA")}
     if orc is not None:
         ref = orc.batch_mat_mul_unified(raw, fmt, X, rows, batch, cols).reshape(batch, rows)
         out["parity"] = parity(got, ref)

@@ -299,7 +299,9 @@ int mmhip_qmm_dev(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat,
  * (cols256 = cols rounded up to 256: e.g. 256 rows of 8192 columns), else
  * MMHIP_ERR_INVALID. Calls on one device share that scratch: calls that
  * overlap on a device (two streams, two contexts, two threads) race. Not
- * timed by mmhip_profile_*. f32 / f16 weights use no scratch. */
+ * timed by mmhip_profile_*. f32 / f16 weights use no scratch, nor do Q8_0
+ * weights of at most 2048 columns (their activations are quantised inside
+ * the one matmul launch; MMHIP_QMM_FUSED=0 turns that off). */
 #define MMHIP_NOALLOC_SCRATCH_BYTES 4456448u
 int mmhip_qmm_dev_noalloc(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat,
                           const float* x_dev, float* y_dev, uint64_t batch,

@@ -2,6 +2,7 @@
 // and the device-pointer GEMV / QMM drivers used by every entry point.
 #include "backend.hpp"
 
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -315,26 +316,47 @@ int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float*
                               (uint32_t)w->cols, ctx->stream);
         return e == hipSuccess ? MMHIP_OK : hip_fail(e, "qmm: launch");
     }
-    e = qscratch->ensure(quant_act_bytes(batch, w->geom.cols_pad));
-    if (e != hipSuccess) return hip_fail(e, "qmm: scratch");
+    if (!qmm_fused(w, batch)) {
+        e = qscratch->ensure(quant_act_bytes(batch, w->geom.cols_pad));
+        if (e != hipSuccess) return hip_fail(e, "qmm: scratch");
+    }
     return qmm_quantised(ctx, w, mat, x, y, batch, out_layout, qscratch->p, true);
+}
+
+bool qmm_fused(const mmhip_weight* w, uint64_t batch) {
+    // MMHIP_QMM_FUSED=0: the two-launch path (quantize_kernel, then
+    // group_kernel) for every shape.
+    static const bool on = [] {
+        const char* e = getenv("MMHIP_QMM_FUSED");
+        return !(e && e[0] == '0');
+    }();
+    // The fused kernel addresses x (batch rows of cols floats) with 32-bit
+    // byte offsets.
+    return on && qmm_q8_fused_fits(w->geom) && batch * w->cols * 4 < 0x80000000ull;
 }
 
 int qmm_quantised(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y, uint64_t batch,
                   int out_layout, void* qbuf, bool timed) {
     const TileGeom& g = w->geom;
+    const uint64_t ld = out_layout == 0 ? w->rows : batch;
+    hipError_t e;
+    if (qmm_fused(w, batch)) {
+        // One launch, the activations quantised inside (qbuf unused).
+        TimedLaunch tl(timed ? ctx : nullptr, "qmm");
+        e = launch_qmm_q8_fused(w->recs, w->dvals, g, mat, x, w->cols, (uint32_t)w->cols, (uint32_t)batch, y, ld,
+                                out_layout, ctx->stream);
+        return e == hipSuccess ? MMHIP_OK : hip_fail(e, "qmm: launch");
+    }
     // The quantiser writes every digit and scale of the batch x cols_pad
     // block it reads back (columns past cols as zeros), so qbuf needs no
     // clearing and keeps nothing from an earlier call.
     const QuantAct q = quant_act_view(qbuf, batch, g.cols_pad);
-    hipError_t e;
     {
         TimedLaunch tl(timed ? ctx : nullptr, "quantize");
         e = launch_quantize(x, w->cols, (uint32_t)batch, (uint32_t)w->cols, (uint32_t)g.cols_pad, q, ctx->stream,
                             g.fmt == kFmtIq2);
     }
     if (e != hipSuccess) return hip_fail(e, "qmm: quantize");
-    const uint64_t ld = out_layout == 0 ? w->rows : batch;
     {
         TimedLaunch tl(timed ? ctx : nullptr, "qmm");
         e = launch_group_dense(w->recs, w->dvals, g, mat, q, (uint32_t)batch, y, ld, out_layout, ctx->num_cu,

@@ -131,8 +131,8 @@ size_t quant_act_bytes(uint64_t n_vec, uint64_t cols_pad);
 int gemv_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t first, uint64_t n, const float* x,
                 uint64_t x_stride, float* y, uint64_t y_stride, DevBuf* qscratch);
 // The quantised branch of qmm_device with the activation digits in `qbuf`
-// (at least quant_act_bytes(batch, cols_pad) bytes); allocates nothing and
-// records no timing events.
+// (at least quant_act_bytes(batch, cols_pad) bytes; unused where qmm_fused
+// holds); allocates nothing, and records timing events only when `timed`.
 int qmm_quantised(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y, uint64_t batch,
                   int out_layout, void* qbuf, bool timed);
 // Kernel arguments of a GEMV over matrices [first, first + n) of a quantised
@@ -141,5 +141,9 @@ GemvArgs gemv_args(const mmhip_weight* w, uint64_t first, uint64_t n, const floa
                    uint64_t y_stride);
 int qmm_device(mmhip_ctx* ctx, const mmhip_weight* w, uint64_t mat, const float* x, float* y,
                uint64_t batch, int out_layout, DevBuf* qscratch);
+// Whether the batched matmul of w runs as one launch with the activation
+// quantisation inside (Q8_0, K <= 2048, x below 2 GiB): then it needs no
+// digit scratch.
+bool qmm_fused(const mmhip_weight* w, uint64_t batch);
 
 }  // namespace mmhip

@@ -336,6 +336,34 @@ __device__ __forceinline__ float max8_lanes(float v) {
     return v;
 }
 
+// The same maxima for non-negative inputs (+Inf and positive NaN patterns
+// allowed): such floats order as their bit patterns do (a NaN above +Inf), so
+// the max is an integer max of the bits, which DPP feeds directly (no
+// canonicalising moves between steps).
+template <int CTRL>
+__device__ __forceinline__ uint32_t umax_dpp(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+    return v > o ? v : o;
+}
+__device__ __forceinline__ float max8_lanes_nonneg(float x) {
+    uint32_t v = __float_as_uint(x);
+    v = umax_dpp<0xB1>(v);
+    v = umax_dpp<0x4E>(v);
+    v = umax_dpp<0x141>(v);
+    return __uint_as_float(v);
+}
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+    uint32_t v = __float_as_uint(x);
+    v = umax_dpp<0xB1>(v);
+    v = umax_dpp<0x4E>(v);
+    v = umax_dpp<0x141>(v);
+    v = umax_dpp<0x140>(v);
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = p[0] > p[1] ? p[0] : p[1];
+    const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __uint_as_float(q[0] > q[1] ? q[0] : q[1]);
+}
+
 // Activation quantisation for the decode kernels: one 32-column block per 8
 // lanes, 4 columns per lane. A block's scale is s = max|x| / 32512 and each
 // column becomes q = rint(x / s) in [-32512, 32512], split into int8 digits
@@ -344,33 +372,48 @@ __device__ __forceinline__ float max8_lanes(float v) {
 // every output that reads them; blocks below 2^-100 are all zero. The
 // reciprocal need not be correctly rounded: q is clamped, and the error stays
 // far below the half-step rounding error.
-__device__ __forceinline__ float quantize_quad(const float (&v)[4], uint32_t& hi4, uint32_t& lo4) {
-    float m = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) m = fmaxf(m, (v[e] != v[e]) ? __uint_as_float(0x7F800000u) : fabsf(v[e]));
-    m = max8_lanes(m);
-    float scale, inv;
-    if (!(m <= 3.4028235e38f)) {
-        scale = __uint_as_float(0x7FC00000u);
-        inv = 0.0f;
-    } else if (m < 0x1p-100f) {
-        scale = 0.0f;
-        inv = 0.0f;
-    } else {
-        scale = m * (1.0f / kDigitMax);
-        inv = __builtin_amdgcn_rcpf(scale);
-    }
-    hi4 = 0;
-    lo4 = 0;
+//
+// The largest |x| of this lane's four columns as bits: |x| of a finite or
+// infinite x orders as its bit pattern, and a NaN's pattern lies above +Inf,
+// so the block's maximum is non-finite exactly when one of its x is.
+__device__ __forceinline__ uint32_t quad_abs_max_bits(const float (&v)[4]) {
+    uint32_t m = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const float qf = fminf(fmaxf(rintf(v[e] * inv), -kDigitMax), kDigitMax);
-        const int q = (inv == 0.0f) ? 0 : (int)qf;
-        const int h = (q + 128) >> 8;
-        const int l = q - h * 256;
-        hi4 |= (uint32_t)(h & 0xFF) << (8 * e);
-        lo4 |= (uint32_t)(l & 0xFF) << (8 * e);
+        const uint32_t a = __float_as_uint(v[e]) & 0x7FFFFFFFu;
+        m = a > m ? a : m;
     }
+    return m;
+}
+// Scale and reciprocal of a block from its max |x| (bits); inv = 0 marks a
+// block whose digits are all zero.
+__device__ __forceinline__ float quad_scale(uint32_t m_bits, float& inv) {
+    const float m = __uint_as_float(m_bits);
+    const bool bad = m_bits >= 0x7F800000u;  // Inf or NaN
+    const bool tiny = m < 0x1p-100f;
+    const float sc = m * (1.0f / kDigitMax);
+    const float iv = __builtin_amdgcn_rcpf(sc);
+    inv = (bad || tiny) ? 0.0f : iv;
+    return bad ? __uint_as_float(0x7FC00000u) : (tiny ? 0.0f : sc);
+}
+// The four columns' digits: with q' = q + 128 (|q'| < 2^15), hi is byte 1 of
+// q' and lo is byte 0 of q' with its top bit flipped ((q' mod 256) - 128 =
+// q - 256 hi), so two byte permutes gather the four q' into 16-bit pairs and
+// two more pick the hi and the lo bytes.
+__device__ __forceinline__ void quad_digits(const float (&v)[4], float inv, uint32_t& hi4, uint32_t& lo4) {
+    int q[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = (int)fminf(fmaxf(rintf(v[e] * inv), -kDigitMax), kDigitMax) + 128;
+    const uint32_t a = __builtin_amdgcn_perm((uint32_t)q[1], (uint32_t)q[0], 0x05040100u);
+    const uint32_t b = __builtin_amdgcn_perm((uint32_t)q[3], (uint32_t)q[2], 0x05040100u);
+    const bool zero = inv == 0.0f;
+    hi4 = zero ? 0u : __builtin_amdgcn_perm(b, a, 0x07050301u);
+    lo4 = zero ? 0u : __builtin_amdgcn_perm(b, a, 0x06040200u) ^ 0x80808080u;
+}
+__device__ __forceinline__ float quantize_quad(const float (&v)[4], uint32_t& hi4, uint32_t& lo4) {
+    float inv;
+    const float scale = quad_scale(__float_as_uint(max8_lanes_nonneg(__uint_as_float(quad_abs_max_bits(v)))), inv);
+    quad_digits(v, inv, hi4, lo4);
     return scale;
 }
 
@@ -379,32 +422,9 @@ __device__ __forceinline__ float quantize_quad(const float (&v)[4], uint32_t& hi
 // over 64 lanes. Used where the consumer applies one activation scale per
 // 256-column record unit (the grouped IQ2_XXS matmul).
 __device__ __forceinline__ float quantize_quad_wave(const float (&v)[4], uint32_t& hi4, uint32_t& lo4) {
-    float m = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) m = fmaxf(m, (v[e] != v[e]) ? __uint_as_float(0x7F800000u) : fabsf(v[e]));
-    m = wave_max(m);
-    float scale, inv;
-    if (!(m <= 3.4028235e38f)) {
-        scale = __uint_as_float(0x7FC00000u);
-        inv = 0.0f;
-    } else if (m < 0x1p-100f) {
-        scale = 0.0f;
-        inv = 0.0f;
-    } else {
-        scale = m * (1.0f / kDigitMax);
-        inv = __builtin_amdgcn_rcpf(scale);
-    }
-    hi4 = 0;
-    lo4 = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float qf = fminf(fmaxf(rintf(v[e] * inv), -kDigitMax), kDigitMax);
-        const int q = (inv == 0.0f) ? 0 : (int)qf;
-        const int h = (q + 128) >> 8;
-        const int l = q - h * 256;
-        hi4 |= (uint32_t)(h & 0xFF) << (8 * e);
-        lo4 |= (uint32_t)(l & 0xFF) << (8 * e);
-    }
+    float inv;
+    const float scale = quad_scale(__float_as_uint(wave_max_nonneg(__uint_as_float(quad_abs_max_bits(v)))), inv);
+    quad_digits(v, inv, hi4, lo4);
     return scale;
 }
 

@@ -366,6 +366,145 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG == 512) ? 4 : 2) void gro
     }
 }
 
+// Dense Q8_0 matmul for K <= 2048 with the activation quantisation fused in
+// and each tile's K range split over KS waves. A workgroup is one item (8
+// activation rows) and 16 / KS row tiles; wave (ts, ks) streams units
+// [ks * units / KS, (ks + 1) * units / KS) of tile ts (one or two steps of
+// four units), all issued before the first product, so a wave waits for its
+// weights once. The workgroup quantises its item's rows straight into the
+// LDS A layout (quantize_quad: the digits and scales quantize_kernel
+// writes), so the call is one launch. Partial sums of a tile are added in
+// slice order (ks = 0, 1, ..) by its first wave.
+struct QmmQ8Args {
+    const uint4* recs;
+    const uint16_t* dvals;
+    uint64_t rec_stride, d_stride;
+    uint32_t d_row;
+    const float* x;
+    uint32_t x_stride;              // floats between rows
+    uint32_t x_bytes;               // batch rows of x (< 2^31)
+    uint32_t cols;                  // columns of x read (a multiple of 32; past them: zeros)
+    float* y;
+    uint64_t y_slot, y_row;         // y[b * y_slot + r * y_row]
+    uint64_t mat;
+    uint32_t batch, tiles, units, rows;
+    uint32_t tgroups;               // ceil(tiles / (16 / KS))
+};
+
+template <int KS>
+__global__ __launch_bounds__((16 / KS) * KS * 64) void qmm_q8_fused_kernel(QmmQ8Args a) {
+    constexpr int UPS = 4;  // Q8_0 steps load their scales as 16-byte words
+    constexpr uint32_t kTpw = 16 / KS;      // tiles per workgroup
+    constexpr uint32_t kWaves = kTpw * KS;  // 14..16
+    constexpr uint32_t kPasses = (kGChunkBlocks + kWaves - 1) / kWaves;
+    __shared__ __align__(16) uint8_t aq[kGChunkBlocks * 512];
+    __shared__ __align__(16) float xs_lds[kGRows * kGChunkBlocks];
+    __shared__ float red[KS > 1 ? kTpw * (KS - 1) * 2 * 64 : 1];
+
+    // Block b -> (item, tile group): the eight workgroups b = 8 r + x (one
+    // per XCD) take tile groups 8 (r / items) + x of item r % items, so each
+    // XCD's L2 holds one eighth of the matrix for every item.
+    const uint32_t n_items = (a.batch + kGRows - 1) / kGRows;
+    const uint32_t xcd = blockIdx.x & 7, r8 = blockIdx.x >> 3;
+    const uint32_t item = r8 % n_items, tg = (r8 / n_items) * 8 + xcd;
+    if (tg >= a.tgroups) return;  // whole workgroup
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t n = lane & 15, g = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ts = wave / KS, ks = wave % KS;
+    const uint32_t tile = tg * kTpw + ts;
+    const uint32_t first = item * kGRows, count = min(a.batch - first, kGRows);
+    const uint32_t nblk = a.units * 2;  // <= kGChunkBlocks (host)
+
+    // ---- Activation loads first. Pass p of wave w covers block
+    // b = w + kWaves p of the item's 8 rows: lane l holds row j = l / 8,
+    // columns 4 (l % 8) .. + 3 of the block, one 16-byte load (cols is a
+    // multiple of 32, so a quad is wholly inside or outside the row; outside
+    // reads zeros; rows past the item read zeros).
+    const uint32_t j = lane >> 3, jq = lane & 7;
+    const BufRsrc x_r = make_rsrc(a.x, a.x_bytes);
+    const uint32_t x_row = (first + j) * a.x_stride * 4 + 16 * jq;  // < 2^31 where used (host)
+    float xv[kPasses][4];
+#pragma unroll
+    for (uint32_t p = 0; p < kPasses; ++p) {
+        const uint32_t b = wave + kWaves * p;
+        const bool ok = j < count && b * 32 + 4 * jq < a.cols;
+        const uint4 v = buf_load_b128(x_r, ok ? x_row + b * 128 : kBufOob, 0);
+        xv[p][0] = __uint_as_float(v.x);
+        xv[p][1] = __uint_as_float(v.y);
+        xv[p][2] = __uint_as_float(v.z);
+        xv[p][3] = __uint_as_float(v.w);
+    }
+    __builtin_amdgcn_s_barrier();  // every wave's activation loads ahead of the weights
+
+    // ---- This wave's weight steps, all in flight at once.
+    const uint32_t upk = a.units / KS, steps = upk / UPS;  // steps <= 2 (host)
+    const uint32_t u0 = ks * upk;
+    const BufRsrc rec_r = make_rsrc(a.recs + a.mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
+    const BufRsrc d_r = make_rsrc(a.dvals + a.mat * a.d_stride, (uint32_t)(a.d_stride * 2));
+    const uint32_t rec_voff = lane * 16, d_voff = n * a.d_row * 2;
+    const bool tile_ok = tile < a.tiles;
+    uint4 rr[2][kMaxUnitsPerStep];
+    uint32_t dd[2][kMaxUnitsPerStep];
+#pragma unroll
+    for (uint32_t s = 0; s < 2; ++s) {
+        const uint32_t u = u0 + s * UPS;
+        const bool ok = tile_ok && s < steps;
+        load_step<kFmtQ8, UPS>(rec_r, rec_voff, ok ? (tile * a.units + u) * 1024 : kBufOob, d_r, d_voff,
+                               ok ? (tile * 16 * a.d_row + 2 * u) * 2 : kBufOob, rr[s], dd[s]);
+    }
+
+    // ---- Quantise the item's rows into the LDS A layout: A row 2j / 2j + 1
+    // = row j's hi / lo digits; lane (n, g) of block pair bp holds columns
+    // 8g .. 8g + 7 of blocks 2 bp (bytes 0..7) and 2 bp + 1 (bytes 8..15).
+    uint8_t* const a_lane = aq + ((jq >> 1) * 16 + 2 * j) * 16 + (jq & 1) * 4;
+#pragma unroll
+    for (uint32_t p = 0; p < kPasses; ++p) {
+        const uint32_t b = wave + kWaves * p;
+        if (b < nblk) {  // whole wave (blocks past the padded row are never read)
+            uint32_t h4, l4;
+            const float sc = quantize_quad(xv[p], h4, l4);
+            uint8_t* const dst = a_lane + (b >> 1) * 1024 + (b & 1) * 8;
+            *reinterpret_cast<uint32_t*>(dst) = h4;
+            *reinterpret_cast<uint32_t*>(dst + 16) = l4;
+            if (jq == 0) xs_lds[j * kGChunkBlocks + b] = sc;
+        }
+    }
+    lds_barrier();
+
+    float acc0 = 0.0f, acc1 = 0.0f;
+    const float* xs0 = xs_lds + (2 * g) * kGChunkBlocks;
+    const float* xs1 = xs0 + kGChunkBlocks;
+#pragma unroll
+    for (uint32_t s = 0; s < 2; ++s)
+        if (s < steps) step_group_q8<UPS>(rr[s], dd[s], u0 + s * UPS, aq, xs0, xs1, lane, acc0, acc1);
+
+    if (KS > 1) {
+        if (ks > 0) {
+            float* rp = red + ((ts * (KS - 1) + (ks - 1)) * 2) * 64;
+            rp[lane] = acc0;
+            rp[64 + lane] = acc1;
+        }
+        lds_barrier();
+        if (ks > 0) return;
+#pragma unroll
+        for (uint32_t k = 1; k < KS; ++k) {
+            const float* rp = red + ((ts * (KS - 1) + (k - 1)) * 2) * 64;
+            acc0 += rp[lane];
+            acc1 += rp[64 + lane];
+        }
+    }
+    const uint32_t row = tile * 16 + n;
+    if (tile_ok && row < a.rows) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t jr = 2 * g + h;
+            if (jr < count) a.y[(uint64_t)(first + jr) * a.y_slot + (uint64_t)row * a.y_row] = h ? acc1 : acc0;
+        }
+    }
+}
+
 template <int FMT, int WG>
 const void* group_kernel_for(int ups) {
     switch (ups) {
@@ -466,6 +605,62 @@ hipError_t launch_group_dense(const uint4* recs, const uint16_t* dvals, const Ti
     a.y_slot = out_layout == 0 ? y_ld : 1;
     a.y_row = out_layout == 0 ? 1 : y_ld;
     return launch(a, g.fmt, (batch + kGRows - 1) / kGRows, num_cu, s);
+}
+
+// K slices per tile for the fused Q8_0 matmul: slices of two four-unit steps
+// where the units split that way, else of one step (16 / slices tiles per
+// workgroup); 0 for K above one LDS chunk (2048 columns) or units not a
+// multiple of four.
+static uint32_t qmm_q8_slices(const TileGeom& g) {
+    if (g.fmt != kFmtQ8 || g.units == 0 || g.units * 2 > kGChunkBlocks || g.units % 4) return 0;
+    return (uint32_t)(g.units % 8 == 0 ? g.units / 8 : g.units / 4);  // 1..7 (units <= 32)
+}
+
+bool qmm_q8_fused_fits(const TileGeom& g) { return qmm_q8_slices(g) != 0; }
+
+hipError_t launch_qmm_q8_fused(const uint4* recs, const uint16_t* dvals, const TileGeom& g, uint64_t mat,
+                               const float* x, uint64_t x_stride, uint32_t cols, uint32_t batch, float* y,
+                               uint64_t y_ld, int out_layout, hipStream_t s) {
+    if (batch == 0) return hipSuccess;
+    const uint32_t ks = qmm_q8_slices(g);
+    // x is addressed with 32-bit byte offsets from one buffer resource.
+    const uint64_t x_bytes = ((uint64_t)(batch - 1) * x_stride + cols) * 4;
+    if (ks == 0 || cols > g.cols_pad || cols % 32 || x_stride < cols || g.tiles == 0 || x_bytes >= kBufOob)
+        return hipErrorInvalidValue;
+    QmmQ8Args a{};
+    a.recs = recs;
+    a.dvals = dvals;
+    a.rec_stride = g.rec_stride;
+    a.d_stride = g.d_stride;
+    a.d_row = (uint32_t)g.d_row;
+    a.x = x;
+    a.x_stride = (uint32_t)x_stride;
+    a.x_bytes = (uint32_t)x_bytes;
+    a.cols = cols;
+    a.y = y;
+    a.y_slot = out_layout == 0 ? y_ld : 1;
+    a.y_row = out_layout == 0 ? 1 : y_ld;
+    a.mat = mat;
+    a.batch = batch;
+    a.tiles = (uint32_t)g.tiles;
+    a.units = (uint32_t)g.units;
+    a.rows = (uint32_t)g.rows;
+    const uint32_t tpw = 16 / ks;
+    a.tgroups = (a.tiles + tpw - 1) / tpw;
+    const uint64_t items = (batch + kGRows - 1) / kGRows;
+    const uint64_t groups8 = (a.tgroups + 7) / 8;
+    const uint64_t blocks = groups8 * items * 8;
+    if (blocks > 0x7FFFFFFFu) return hipErrorInvalidValue;
+    const void* fns[8] = {nullptr,
+                          reinterpret_cast<const void*>(&qmm_q8_fused_kernel<1>),
+                          reinterpret_cast<const void*>(&qmm_q8_fused_kernel<2>),
+                          reinterpret_cast<const void*>(&qmm_q8_fused_kernel<3>),
+                          reinterpret_cast<const void*>(&qmm_q8_fused_kernel<4>),
+                          reinterpret_cast<const void*>(&qmm_q8_fused_kernel<5>),
+                          reinterpret_cast<const void*>(&qmm_q8_fused_kernel<6>),
+                          reinterpret_cast<const void*>(&qmm_q8_fused_kernel<7>)};
+    void* args[] = {&a};
+    return hipLaunchKernel(fns[ks], dim3((unsigned)blocks), dim3(tpw * ks * 64), args, 0, s);
 }
 
 hipError_t launch_group_experts(const uint4* recs, const uint16_t* dvals, const TileGeom& g, const QuantAct& xq,

@@ -222,6 +222,15 @@ hipError_t launch_gemv_float(const void* w, uint32_t ggml_type, uint64_t mat_str
 hipError_t launch_group_dense(const uint4* recs, const uint16_t* dvals, const TileGeom& g, uint64_t mat,
                               const QuantAct& xq, uint32_t batch, float* y, uint64_t y_ld, int out_layout,
                               int num_cu, hipStream_t s);
+// Dense Q8_0 in one launch (the activations quantised inside, each tile's K
+// range split over waves): Y = X . W^T as launch_group_dense computes it
+// from launch_quantize's output, for the shapes qmm_q8_fused_fits accepts
+// (K <= 2048 columns). x rows are x_stride floats apart; columns >= cols
+// read as zero.
+bool qmm_q8_fused_fits(const TileGeom& g);
+hipError_t launch_qmm_q8_fused(const uint4* recs, const uint16_t* dvals, const TileGeom& g, uint64_t mat,
+                               const float* x, uint64_t x_stride, uint32_t cols, uint32_t batch, float* y,
+                               uint64_t y_ld, int out_layout, hipStream_t s);
 // Grouped: item i < *n_work multiplies activation rows a_row[slot ..
 // slot + count) (a_row null: the slots themselves) by matrix work[i].mat and
 // writes y[(slot + j) * y_ld + pad + r]. max_work bounds the grid.

@@ -213,6 +213,35 @@ def test_qmm_ragged_batches_and_layouts(ctx, orc, batch):
     dy.free()
 
 
+@pytest.mark.parametrize("cols", [256, 768, 1024, 1280, 1536, 1792, 2048, 2304])
+def test_qmm_q8_every_k_split(ctx, orc, cols):
+    """Q8_0 matmul over every K width the one-launch kernel splits its own
+    way (units of 64 columns per 16-row tile: 4 -> one slice, 12 -> three
+    one-step slices, 16 -> two, 20 -> five, 24 -> three two-step slices,
+    28 -> seven, 32 -> four) and one past it (2304: the two-launch path),
+    with a ragged batch and ragged rows, both output layouts, against the
+    oracle's matMulQ8_0 (qmm.zig:58-138)."""
+    rng = np.random.default_rng(cols)
+    rows, batch = 100, 13
+    raw = _weights(rng, mm.Q8_0, rows, cols)
+    xin = rng.standard_normal((batch, cols)).astype(np.float32)
+    ref_mn = orc.matmul_q8_0(raw, xin, rows, batch, cols)
+    w = ctx.upload(raw, mm.Q8_0, rows, cols)
+    dx = mm.DeviceArray.from_numpy(ctx, xin)
+    dy = mm.DeviceArray(ctx, rows * batch * 4)
+    try:
+        for layout in (0, 1):
+            ctx.qmm_dev(w, 0, dx, dy, batch, layout)
+            ctx.synchronize()
+            y = dy.to_numpy(np.float32, rows * batch)
+            y = y.reshape(batch, rows).T if layout == 0 else y.reshape(rows, batch)
+            assert mm.max_abs_rel(y, ref_mn) <= TOL_QMM, (cols, layout)
+    finally:
+        w.free()
+        dx.free()
+        dy.free()
+
+
 def test_qmm_reference_kats(ctx, orc):
     # qmm.zig:142-173: 4x8x64 all-ones -> 64 +- 0.1
     d, _ = orc.f32_to_f16(1.0 / 127.0)
