@@ -53,7 +53,10 @@ __device__ void route_body(const RouteArgs& a, RouteLds& L) {
         s_cnt[e] = 0;
         s_rec[e] = 0;
     }
-    __syncthreads();
+    // Every barrier here orders LDS only: no phase reads what an earlier one
+    // stored to global memory, and __syncthreads() would also wait for every
+    // wave's outstanding global stores and statistics atomics (~1 us each).
+    lds_barrier();
 
     // Four tokens per wave, one per 16-lane row (route_row16); the row's
     // first lane writes the token's results.
@@ -80,7 +83,7 @@ __device__ void route_body(const RouteArgs& a, RouteLds& L) {
             a.slot_tok[4 * T + t] = t;
         }
     }
-    __syncthreads();
+    lds_barrier();
     // Statistics: one device atomic per recorded expert.
     for (uint32_t e = tid; e < E; e += kRouteThreads)
         if (s_rec[e]) atomicAdd(a.counts + e, (unsigned long long)s_rec[e]);
@@ -118,7 +121,7 @@ __device__ void route_body(const RouteArgs& a, RouteLds& L) {
         const uint32_t t = p / kMaxK, i = p % kMaxK;
         if (i < k && ((s_act[t] >> i) & 1u)) s_rank[p] = atomicAdd(&s_cnt[s_ids[p]], 1u);
     }
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
         // Exclusive scans over experts: slot offsets and chunk (work item) offsets.
         uint32_t carry = 0, carry_ch = 0;
@@ -145,7 +148,7 @@ __device__ void route_body(const RouteArgs& a, RouteLds& L) {
         }
         if (lane == 0) L.nchunks = carry_ch;
     }
-    __syncthreads();
+    lds_barrier();
     for (uint32_t p = tid; p < T * kMaxK; p += kRouteThreads) {
         const uint32_t t = p / kMaxK, i = p % kMaxK;
         if (i < k && ((s_act[t] >> i) & 1u)) {
