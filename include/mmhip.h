@@ -109,6 +109,9 @@ int mmhip_memset_dev(mmhip_ctx* ctx, void* dst_dev, int value, size_t bytes);
  * `count` stacks matrices of [rows x cols] back to back, as the expert
  * tensors ffn_{gate,up,down}_exps are stored ([n_experts][rows][cols],
  * src/inference.zig:1148-1166).
+ * One repacked Q8_0 / IQ2_XXS matrix must stay below 2 GiB (about 2e9
+ * Q8_0 weights); a larger one is MMHIP_ERR_UNSUPPORTED. `count` is not
+ * limited by this.
  * ====================================================================== */
 
 int mmhip_weight_upload(mmhip_ctx* ctx, const void* raw_host, uint32_t type,

@@ -200,6 +200,13 @@ int weight_create_segments(mmhip_ctx* ctx, const WeightSegment* segs, size_t n_s
     // fetches a row's scales for several units.
     g.d_row = ((g.units * ((type == kIq2Xxs) ? 1 : 2) + 7) / 8) * 8;
     g.d_stride = g.tiles * 16 * g.d_row;
+    // Every kernel reads one matrix through a buffer resource with 32-bit
+    // offsets, 2^31 being its out-of-range sentinel.
+    if (g.rec_stride * 16 >= 0x80000000ull || g.d_stride * 2 >= 0x80000000ull) {
+        delete w;
+        set_error(MMHIP_ERR_UNSUPPORTED, "weight: one repacked matrix must stay below 2 GiB");
+        return MMHIP_ERR_UNSUPPORTED;
+    }
     const size_t rec_bytes = (size_t)(g.rec_stride * count * 16);
     const size_t d_bytes = (size_t)(g.d_stride * count * 2);
     e = hipMalloc(&w->recs, rec_bytes);

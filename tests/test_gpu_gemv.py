@@ -347,6 +347,18 @@ def test_gemv_grouped_rejects_bad_groups(ctx):
             a.free()
 
 
+def test_weight_over_2gib_per_matrix_is_rejected(ctx):
+    # 2^21 rows of 1024 Q8_0 columns repack to exactly 2 GiB of records; the
+    # kernels address one matrix with 32-bit offsets, so the upload refuses it
+    # before allocating. The source is a full-size zero buffer (calloc, pages
+    # untouched) so that a missing check would still read only valid memory.
+    rows, cols = 1 << 21, 1024
+    raw = np.zeros(rows * (cols // 32) * 34, np.uint8)
+    with pytest.raises(mm.MmhipError) as e:
+        ctx.upload(raw, mm.Q8_0, rows, cols)
+    assert e.value.code == mm.ERR_UNSUPPORTED
+
+
 @pytest.mark.parametrize("t", [mm.IQ2_XXS, mm.Q8_0])
 def test_headline_step_shape_matches_oracle(ctx, orc, t):
     """The benchmark's headline launch exactly as it is measured: one
