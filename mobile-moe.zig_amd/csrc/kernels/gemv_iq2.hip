@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     struct Lds {
         uint32_t tab[kIq2TableWords];
         uint32_t mtab[8];  // hi3 sign masks
-        float part[kQMaxItems * 64];
+        alignas(16) float part[kQMaxItems * 64];  // per item: row n's lane groups g at 4 n + g
         uint8_t aq[kQChunkBlocks * 64];
         float xs[kQChunkBlocks];
         float row_sum[kQMaxTiles * 16];
@@ -163,6 +163,9 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     const uint32_t rec_voff = lane * 16;
     const uint32_t d_voff = n * a.d_row * 2;
     const uint32_t rec_tile = keep_sgpr(a.units * 1024u), d_tile = keep_sgpr(a.d_row * 32u);
+    // This lane's word in an item's 64 partials: row-major (4 n + g), so the
+    // row sums read each row's four lane groups as one 16-byte word.
+    const uint32_t part_slot = (n << 2) | g;
     // Sparse A row of this lane: block s_star of the unit, digit d_star.
     const uint32_t s_star = (n >> 2) + 4 * ((n >> 1) & 1u), d_star = n & 1u;
 
@@ -308,19 +311,20 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
                     const float sb = fmaf((float)iq2_ls_b(r), xb, hb);
                     float v = (float)digits_combine(acc[0], acc[1]) * sa;
                     v = fmaf((float)digits_combine(acc[2], acc[3]), sb, v);
-                    part[(cur.ul * n_tiles + cur.t) * 64 + lane] = v * df;
+                    part[(cur.ul * n_tiles + cur.t) * 64 + part_slot] = v * df;
                     cur = advance(cur);
                 }
             }
         }
         lds_barrier();  // every item's partials written
-        // Row sums: units in order, lane groups in order.
+        // Row sums: units in order, lane groups in order (one 16-byte read
+        // per unit; a wave's lanes read consecutive words, no bank conflicts).
         for (uint32_t idx = threadIdx.x; idx < n_tiles * 16; idx += kQWg) {
             const uint32_t t = idx >> 4, rr = idx & 15;
             float sum = 0.0f;
             for (uint32_t ul = 0; ul < uc; ++ul) {
-                const float* pp = part + (ul * n_tiles + t) * 64 + rr;
-                sum += ((pp[0] + pp[16]) + pp[32]) + pp[48];
+                const float4 q = *reinterpret_cast<const float4*>(part + (ul * n_tiles + t) * 64 + rr * 4);
+                sum += ((q.x + q.y) + q.z) + q.w;
             }
             row_sum[idx] += sum;
         }
@@ -382,7 +386,7 @@ __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineA
         uint32_t mtab[8];
         uint8_t aq[kDcMaxItems * 8 * 64];
         float xs[kDcMaxItems * 8];
-        float part[kDcMaxItems * 64];
+        alignas(16) float part[kDcMaxItems * 64];  // per item: row n's lane groups g at 4 n + g
         float ysum[kDcMaxProbs * 16];
         float cw[kMaxK];        // route weights of the computed entries
         int32_t cs[kMaxK + 1];  // their slots, then the shared slot (-1: none)
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineA
     for (uint32_t j = 0; j < kDcItemsPerWave; ++j) {
         const uint32_t i = wave + kDcWaves * j;
         if (i >= n_items) break;
-        lds.part[i * 64 + lane] = iq2_item(rb[j], db[j], lds.aq + i * 8 * 64, lds.xs + i * 8, lds.tab, lds.mtab, n, g);
+        lds.part[i * 64 + ((n << 2) | g)] = iq2_item(rb[j], db[j], lds.aq + i * 8 * 64, lds.xs + i * 8, lds.tab, lds.mtab, n, g);
     }
     lds_barrier();
     if (threadIdx.x < 16 * kDcMaxProbs) {
@@ -502,8 +506,8 @@ __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineA
         if (p < n_act) {
             float sum = 0.0f;
             for (uint32_t u = 0; u < units; ++u) {
-                const float* pp = lds.part + (p * units + u) * 64 + r;
-                sum += ((pp[0] + pp[16]) + pp[32]) + pp[48];
+                const float4 q = *reinterpret_cast<const float4*>(lds.part + (p * units + u) * 64 + r * 4);
+                sum += ((q.x + q.y) + q.z) + q.w;
             }
             lds.ysum[p * 16 + r] = 0.0f + sum;
         }
