@@ -100,6 +100,19 @@ __device__ __forceinline__ uint32_t keep_sgpr(uint32_t v) {
     return v;
 }
 
+// Every field of a GEMV's arguments (GemvArgs) that a workgroup reads before
+// its first weight load, read at once: the asm takes them all in SGPRs, so
+// their scalar loads go out as one batch with one wait. Read where first
+// used, each early-exit branch waited for its own loads: a chain of six
+// kernel-argument round trips, about 1 us, before the first vector load.
+template <class Args>
+__device__ __forceinline__ void pin_gemv_args(const Args& a) {
+    asm volatile("" ::"s"(a.recs), "s"(a.dvals), "s"(a.rec_stride), "s"(a.d_stride), "s"(a.d_row), "s"(a.x),
+                 "s"(a.x_stride), "s"(a.x2_off), "s"(a.silu_mul), "s"(a.y), "s"(a.y_stride), "s"(a.first_mat),
+                 "s"(a.probs), "s"(a.n_active), "s"(a.n_probs), "s"(a.tiles), "s"(a.units), "s"(a.rows),
+                 "s"(a.cols), "s"(a.tiles_per_wg));
+}
+
 // Waits until all of this wave's vector memory loads have returned
 // (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their no-wait maxima).
 // A CU returns vector loads in issue order across all of its workgroups, so

@@ -64,14 +64,12 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
     __shared__ float row_sum[kGemvMaxTiles * 16];
     __shared__ float edge[2][kWaves * 16];
     extern __shared__ __align__(16) uint8_t smem[];
-    // This workgroup's segment and problem within it.
-    uint32_t si = 0;
-#pragma unroll
-    for (int q = 1; q < NSEG; ++q)
-        if (blockIdx.y >= set.y_begin[q]) si = q;
-    const GemvArgs& a = set.seg[si];
+    // This workgroup's segment (grid slice z) and problem within it (row y).
+    const GemvArgs& a = set.seg[NSEG > 1 ? blockIdx.z : 0];
+    pin_gemv_args(a);
     const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
-    if (t_begin >= a.tiles) return;  // whole workgroup: the grid is sized for the widest segment
+    // The grid is sized for the widest and longest segment.
+    if (t_begin >= a.tiles || blockIdx.y >= a.n_probs) return;  // whole workgroup
     constexpr uint32_t kBlkPerUnit = 2;
     const uint32_t nblk_all = a.units * kBlkPerUnit;
     const uint32_t chunk_blk = nblk_all < kChunkBlocks ? nblk_all : kChunkBlocks;
@@ -81,7 +79,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t p = blockIdx.y - set.y_begin[si];
+    const uint32_t p = blockIdx.y;
     uint64_t mat = a.first_mat + p, x_row = p, y_row = p;
     if constexpr (ROUTE) {
         // Every wave routes the token (same result); the problem follows.
@@ -105,9 +103,12 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
             return;  // whole workgroup: no such problem this call
         }
     } else {
-        if (a.n_active && p >= *a.n_active) return;  // whole workgroup: problem not in this call's list
+        // The count and the problem's entry in one round trip (a null list
+        // is a zero-size resource: its load returns zeros, no access).
+        const uint32_t n_act = buf_load_b32(make_rsrc(a.n_active, a.n_active ? 4u : 0u), 0, 0);
+        const uint4 d = buf_load_b128(make_rsrc(a.probs, a.probs ? (p + 1) * 16u : 0u), p * 16u, 0);
+        if (a.n_active && p >= n_act) return;  // whole workgroup: problem not in this call's list
         if (a.probs) {
-            const uint4 d = a.probs[p];
             mat = d.x;
             x_row = d.y;
             y_row = d.z;
@@ -476,17 +477,11 @@ static hipError_t launch_q_set(const GemvArgs* segs, uint32_t n_segs, const void
     GemvSet<N> set{};
     uint32_t y = 0;
     for (uint32_t i = 0; i < (uint32_t)N; ++i) {
-        if (i < n_segs) {
-            set.seg[i] = segs[i];
-            set.y_begin[i] = y;
-            y += segs[i].n_probs;
-        } else {
-            set.seg[i] = segs[0];
-            set.y_begin[i] = 0xFFFFFFFFu;  // never selected
-        }
+        set.seg[i] = segs[i < n_segs ? i : 0];
+        if (i < n_segs && segs[i].n_probs > y) y = segs[i].n_probs;
     }
     void* args[] = {&set};
-    return hipLaunchKernel(fn, dim3(grid_x, y), dim3(wg), args, lds, s);
+    return hipLaunchKernel(fn, dim3(grid_x, y, n_segs), dim3(wg), args, lds, s);
 }
 
 hipError_t launch_gemv_q(const GemvArgs& a, uint32_t fmt, int num_cu, hipStream_t s) {

@@ -93,9 +93,12 @@ __device__ __forceinline__ bool select_problem(const GemvArgs& a, uint32_t p, ui
         }
         return false;
     } else {
-        if (a.n_active && p >= *a.n_active) return false;
+        // The count and the problem's entry in one round trip (a null list
+        // is a zero-size resource: its load returns zeros, no access).
+        const uint32_t n_act = buf_load_b32(make_rsrc(a.n_active, a.n_active ? 4u : 0u), 0, 0);
+        const uint4 d = buf_load_b128(make_rsrc(a.probs, a.probs ? (p + 1) * 16u : 0u), p * 16u, 0);
+        if (a.n_active && p >= n_act) return false;
         if (a.probs) {
-            const uint4 d = a.probs[p];
             mat = d.x;
             x_row = d.y;
             y_row = d.z;
@@ -134,15 +137,13 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
     float* const xs = lds.xs;
     float* const row_sum = lds.row_sum;
 
-    // This workgroup's segment and problem within it.
-    uint32_t si = 0;
-#pragma unroll
-    for (int q = 1; q < NSEG; ++q)
-        if (blockIdx.y >= set.y_begin[q]) si = q;
-    const GemvArgs& a = set.seg[si];
-    const uint32_t py = blockIdx.y - set.y_begin[si];
+    // This workgroup's segment (grid slice z) and problem within it (row y).
+    const GemvArgs& a = set.seg[NSEG > 1 ? blockIdx.z : 0];
+    const uint32_t py = blockIdx.y;
+    pin_gemv_args(a);
     const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
-    if (t_begin >= a.tiles) return;  // whole workgroup: the grid is sized for the widest segment
+    // The grid is sized for the widest and longest segment.
+    if (t_begin >= a.tiles || py >= a.n_probs) return;  // whole workgroup
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t n = lane & 15, g = lane >> 4;
@@ -539,17 +540,11 @@ static hipError_t launch_set(const GemvArgs* segs, uint32_t n_segs, const void* 
     GemvSet<N> set{};
     uint32_t y = 0;
     for (uint32_t i = 0; i < (uint32_t)N; ++i) {
-        if (i < n_segs) {
-            set.seg[i] = segs[i];
-            set.y_begin[i] = y;
-            y += segs[i].n_probs;
-        } else {
-            set.seg[i] = segs[0];
-            set.y_begin[i] = 0xFFFFFFFFu;  // never selected
-        }
+        set.seg[i] = segs[i < n_segs ? i : 0];
+        if (i < n_segs && segs[i].n_probs > y) y = segs[i].n_probs;
     }
     void* args[] = {&set};
-    return hipLaunchKernel(fn, dim3(grid_x, y), dim3(kQWg), args, 0, s);
+    return hipLaunchKernel(fn, dim3(grid_x, y, n_segs), dim3(kQWg), args, 0, s);
 }
 
 }  // namespace

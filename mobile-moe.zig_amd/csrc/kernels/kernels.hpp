@@ -132,13 +132,14 @@ hipError_t launch_quantize(const float* x, uint64_t x_stride, uint32_t n_vec, ui
 hipError_t launch_gemv_q(const GemvArgs& a, uint32_t fmt, int num_cu, hipStream_t s);
 // Up to kGemvMaxSegs such GEMVs of one format in ONE launch: segments may
 // differ in weight, shape, activations and outputs (e.g. a layer's experts'
-// gate/up and down projections). Segment s owns the grid rows
-// [y_begin[s], y_begin[s + 1]). Not for route_decode.
+// gate/up and down projections). Segment s is grid slice blockIdx.z = s and
+// problem p of it grid row p (rows past its n_probs exit at once), so a
+// workgroup finds its arguments without reading any first. Not for
+// route_decode.
 constexpr uint32_t kGemvMaxSegs = 4;
 template <int N>
 struct GemvSet {
     GemvArgs seg[N];
-    uint32_t y_begin[N];
 };
 hipError_t launch_gemv_segments(const GemvArgs* segs, uint32_t n_segs, uint32_t fmt, int num_cu, hipStream_t s);
 // IQ2_XXS decode GEMV (gemv_iq2.hip); launch_gemv_q / launch_gemv_segments
