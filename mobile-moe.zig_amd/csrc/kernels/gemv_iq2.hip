@@ -5,7 +5,7 @@
 // One 1024-thread workgroup per CU owns one problem (matrix + activation
 // vector) and up to kQMaxTiles 16-row tiles (kQMaxItems record units per
 // activation chunk). A launch may hold several segments (weights of
-// different shapes), each owning a range of the grid's problem rows. The activation is quantised into
+// different shapes), each one slice (blockIdx.z) of the grid. The activation is quantised into
 // LDS per K-chunk of up to 8 record units (2048 columns) as two int8 digit
 // planes per 32-column block (x ~ s (256 hi + lo)).
 //
