@@ -253,26 +253,42 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG == 512) ? 4 : 2) void gro
         }
     };
     // Stage chunk [kb, kb + nb) of the item's activations: thread t moves the
-    // 16-byte A words c = t + i * WG and the scales (j, b) = t + i * WG.
+    // 16-byte A words c = t + i * WG (all of activation row ((t & 15) >> 1),
+    // WG being a multiple of 16) and the scales (j, b) = t + i * WG.
     constexpr uint32_t kPer = kGStage / WG;
     constexpr uint32_t kScales = kGRows * kGChunkBlocks;
     constexpr uint32_t kPerSc = (kScales + WG - 1) / WG;
+    static_assert(WG % 16 == 0, "a thread's A words share one activation row");
+    // This thread's activation rows in the current run, read once per run by
+    // load_rows (next_run), before the run's other loads: read inside the
+    // staging loop, each row's load and the wait for it came after the
+    // table and earlier staging loads, and vector loads return in issue
+    // order, so every iteration waited for all of them.
+    uint64_t xrow = 0, srow[kPerSc];
+    auto load_rows = [&]() {
+        xrow = act_row((threadIdx.x & 15) >> 1);
+#pragma unroll
+        for (uint32_t i = 0; i < kPerSc; ++i) {
+            const uint32_t e = threadIdx.x + i * WG;
+            srow[i] = act_row((e < kScales ? e : 0) / kGChunkBlocks);
+        }
+    };
     auto stage_load = [&](uint32_t kb0, uint32_t nb, uint2 (&lo)[kPer], uint2 (&hi)[kPer], float (&sc)[kPerSc]) {
+        const int8_t* plane = (threadIdx.x & 1) ? a.xl : a.xh;
 #pragma unroll
         for (uint32_t i = 0; i < kPer; ++i) {
             const uint32_t c = threadIdx.x + i * WG;
-            const uint32_t p = c >> 6, l = c & 63, ln = l & 15, lg = l >> 4;
+            const uint32_t p = c >> 6, l = c & 63, lg = l >> 4;
             const bool ok = 2 * p < nb;
-            const int8_t* plane = (ln & 1) ? a.xl : a.xh;
-            const int8_t* src = plane + act_row(ln >> 1) * a.xq_stride + (kb0 + 2 * (ok ? p : 0)) * 32 + 8 * lg;
+            const int8_t* src = plane + xrow * a.xq_stride + (kb0 + 2 * (ok ? p : 0)) * 32 + 8 * lg;
             lo[i] = *reinterpret_cast<const uint2*>(src);
             hi[i] = *reinterpret_cast<const uint2*>(src + 32);
         }
 #pragma unroll
         for (uint32_t i = 0; i < kPerSc; ++i) {
             const uint32_t e = threadIdx.x + i * WG;
-            const uint32_t j = (e < kScales ? e : 0) / kGChunkBlocks, b = e % kGChunkBlocks;
-            sc[i] = a.xs[act_row(j) * a.xs_stride + kb0 + (b < nb ? b : 0)];
+            const uint32_t b = e % kGChunkBlocks;
+            sc[i] = a.xs[srow[i] * a.xs_stride + kb0 + (b < nb ? b : 0)];
         }
     };
     auto stage_store = [&](uint32_t nb, const uint2 (&lo)[kPer], const uint2 (&hi)[kPer], const float (&sc)[kPerSc]) {
@@ -311,6 +327,7 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG == 512) ? 4 : 2) void gro
         n_sub = min(a.units, chunk_units) / UPS;
         steps = my_n * n_sub;
         kb = 0;
+        load_rows();
     };
     next_run();
     {
