@@ -170,7 +170,7 @@ __device__ __forceinline__ void step_group_q8(const uint4 (&r)[kMaxUnitsPerStep]
 // 512-thread IQ2_XXS workgroups share a CU (their LDS fits twice), four waves
 // per SIMD, so at most 128 registers.
 template <int FMT, int UPS, int WG>
-__global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG == 512) ? 4 : 2) void group_kernel(GroupArgs a) {
+__global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG >= 512) ? 4 : 2) void group_kernel(GroupArgs a) {
     constexpr uint32_t kWaves = WG / 64;
     constexpr uint32_t kBlkPerUnit = (FMT == kFmtIq2) ? 8 : 2;
     __shared__ __align__(16) uint32_t tab[FMT == kFmtIq2 ? kIq2LdsWords : 4];
@@ -351,6 +351,15 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG == 512) ? 4 : 2) void gro
     for (;;) {
         lds_barrier();
         for (uint32_t s = 0; s < steps; s += 3) {
+            if constexpr (WG == 1024) {
+                // Issue priority by steps left (a SIMD serves its oldest wave
+                // first; the youngest would otherwise end last).
+                const uint32_t rem = steps - s;
+                if (rem > 12) __builtin_amdgcn_s_setprio(3);
+                else if (rem > 6) __builtin_amdgcn_s_setprio(2);
+                else if (rem > 3) __builtin_amdgcn_s_setprio(1);
+                else __builtin_amdgcn_s_setprio(0);
+            }
             compute(s, r0, d0);
             load(s + 3, r0, d0);
             if (s + 1 < steps) compute(s + 1, r1, d1);
@@ -564,21 +573,32 @@ int resident(const void* fn, int wg) {
 
 hipError_t launch(GroupArgs a, uint32_t fmt, uint32_t items, int num_cu, hipStream_t s) {
     if (items == 0 || a.tiles == 0) return hipSuccess;
-    // Workgroup size and step: measured on MI355X at batch 64, IQ2_XXS
+    // Workgroup size and step, measured on MI355X at batch 64: IQ2_XXS
     // grouped experts run ~10% faster with 512 threads and one-unit steps
-    // (98 registers: four waves per SIMD; two-unit steps need 128 and
-    // spill) than with 256 threads and four-unit steps, when the call has at
-    // least one 512-thread workgroup's tiles per CU; smaller calls (an MLA
+    // (four waves per SIMD; two-unit steps need 128 registers and spill)
+    // than with 256 threads and four-unit steps, and 4% faster again with
+    // one 1024-thread workgroup per CU than with two of 512. Of two
+    // workgroups sharing a CU the older one was served first and ended ~10
+    // us before the other (s_memrealtime per workgroup), which then ran
+    // alone on the CU at half the waves. Each size needs its threads' worth
+    // of tiles per CU (16 or 8 waves' worth); smaller calls (an MLA
     // projection at 64 tokens) would leave CUs idle and keep 256 threads.
     // Q8_0 is fastest with 256 / 4.
-    // Override: MMHIP_GROUP_WG (256 | 512).
+    // Override: MMHIP_GROUP_WG (256 | 512 | 1024, the last IQ2_XXS only).
     static const int wg_env = env_int("MMHIP_GROUP_WG", 0);
     const uint64_t cus = (uint64_t)(num_cu > 0 ? num_cu : 256);
-    const bool wide = fmt == kFmtIq2 && (uint64_t)items * a.tiles >= cus * 8;
-    const int wg = wg_env == 512 || wg_env == 256 ? wg_env : (wide ? 512 : 256);
-    const int ups = group_ups(a.units, fmt, wg == 512 ? 1 : 4);
-    const void* fn = fmt == kFmtIq2 ? (wg == 512 ? group_kernel_for<kFmtIq2, 512>(ups) : group_kernel_for<kFmtIq2, 256>(ups))
-                                    : (wg == 512 ? group_kernel_for<kFmtQ8, 512>(ups) : group_kernel_for<kFmtQ8, 256>(ups));
+    const uint64_t tiles_all = (uint64_t)items * a.tiles;
+    const bool wg_ok = wg_env == 256 || wg_env == 512 || (wg_env == 1024 && fmt == kFmtIq2);
+    const int wg = wg_ok                                         ? wg_env
+                   : fmt == kFmtIq2 && tiles_all >= cus * 16 ? 1024
+                   : fmt == kFmtIq2 && tiles_all >= cus * 8  ? 512
+                                                                 : 256;
+    const int ups = group_ups(a.units, fmt, wg >= 512 ? 1 : 4);
+    const void* fn = fmt == kFmtIq2
+                         ? (wg == 1024 ? group_kernel_for<kFmtIq2, 1024>(ups)
+                            : wg == 512 ? group_kernel_for<kFmtIq2, 512>(ups)
+                                        : group_kernel_for<kFmtIq2, 256>(ups))
+                         : (wg == 512 ? group_kernel_for<kFmtQ8, 512>(ups) : group_kernel_for<kFmtQ8, 256>(ups));
     // Every resident workgroup slot of the device, or fewer when the largest
     // possible call has under one tile per wave for each of them; each
     // workgroup takes 1 / grid of the items' tiles (the actual item count
