@@ -47,6 +47,7 @@ struct GroupArgs {
     uint64_t mat;                   // dense: matrix
     uint32_t batch;                 // dense: rows of the batch
     uint32_t tiles, units, rows;
+    uint32_t gap;                   // grouped: tiles of range an item boundary counts for (see below)
 };
 
 // LDS A layout of one chunk: block pair p (blocks 2p, 2p+1) is 1 KiB; lane
@@ -183,10 +184,25 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG >= 512) ? 4 : 2) void gro
     // (the host sizes the grid before the routing runs). A range covers whole
     // or partial tile runs of one or two items; the activations are staged
     // once per item run.
+    //
+    // A range that crosses into a new item pays for the switch (the pipeline
+    // drains, then the item's work entry, rows, digits and first weights come
+    // in series: ~5.5 steps per wave, s_memrealtime per workgroup), and the
+    // workgroups that cross set the launch's end. So the ranges are cut
+    // equally on a line where every item counts a.gap extra tiles after its
+    // own: a crossing workgroup gets about a switch's worth fewer tiles.
+    // Virtual position v maps to item v / V, tile min(v % V, tiles): the
+    // map is monotone and onto, so the ranges still cover every (item, tile)
+    // exactly once.
     const uint32_t n_items = a.work ? *a.n_work : (a.batch + kGRows - 1) / kGRows;
-    const uint64_t total = (uint64_t)n_items * a.tiles;
-    uint64_t q = total * blockIdx.x / gridDim.x;
-    const uint64_t q_end = total * (blockIdx.x + 1) / gridDim.x;
+    const uint64_t vlen = (uint64_t)a.tiles + a.gap;
+    const uint64_t total_v = (uint64_t)n_items * vlen;
+    auto real_pos = [&](uint64_t v) {
+        const uint64_t it = v / vlen, off = v % vlen;
+        return it * a.tiles + (off < a.tiles ? off : a.tiles);
+    };
+    uint64_t q = real_pos(total_v * blockIdx.x / gridDim.x);
+    const uint64_t q_end = real_pos(total_v * (blockIdx.x + 1) / gridDim.x);
     if (q >= q_end) return;  // whole workgroup
 
     const uint32_t lane = threadIdx.x & 63;
@@ -203,7 +219,7 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG >= 512) ? 4 : 2) void gro
     // v + kWaves i).
     uint64_t mat = a.mat;
     uint32_t first = 0, count = 0, col_off = 0, t_begin = 0, my_n = 0;
-    BufRsrc rec_r, d_r;
+    BufRsrc rec_r = make_rsrc(a.recs, 0u), d_r = make_rsrc(a.dvals, 0u);  // set by next_run
     // Activation row of item row j (rows past `count` repeat row 0: their
     // results are computed and dropped).
     auto act_row = [&](uint32_t j) -> uint64_t {
@@ -604,6 +620,18 @@ hipError_t launch(GroupArgs a, uint32_t fmt, uint32_t items, int num_cu, hipStre
     // workgroup takes 1 / grid of the items' tiles (the actual item count
     // of a grouped call is only known on the device).
     const uint32_t waves = wg / 64;
+    // An item switch costs a 1024-thread workgroup ~5.5 steps per wave
+    // (batch-64 MoE layer, both grouped launches); in tiles of a workgroup's
+    // range that is 5.5 x waves / (steps per tile). Measured there: 1.34 ->
+    // 1.27 us per token. Dense calls with 256 threads (the MLA projections at
+    // 64 tokens) ran slower with such a gap (48.5 -> 58.0 us per layer) and
+    // keep ranges of equal tiles. MMHIP_GROUP_SWITCH_TENTHS: the cost in
+    // tenths of a step (0: equal tiles).
+    static const int sw_env = env_int("MMHIP_GROUP_SWITCH_TENTHS", 55);
+    const uint64_t steps_per_tile = a.units / (uint32_t)ups > 0 ? a.units / (uint32_t)ups : 1;
+    a.gap = (sw_env > 0 && wg == 1024 && a.work)
+                ? (uint32_t)(((uint64_t)sw_env * waves + 5 * steps_per_tile) / (10 * steps_per_tile))
+                : 0u;
     const uint64_t slots = cus * resident(fn, wg);
     const uint64_t most = ((uint64_t)items * a.tiles + waves - 1) / waves;
     const dim3 grid((unsigned)(most < slots ? most : slots));
