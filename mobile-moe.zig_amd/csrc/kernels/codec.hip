@@ -200,8 +200,12 @@ __global__ __launch_bounds__(256) void quantize_wide_kernel(const float* __restr
                                                              int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                              float* __restrict__ sc, uint64_t q_stride,
                                                              uint64_t s_stride) {
+    // All arguments in one batch of scalar loads (the early exit below
+    // otherwise waited for its own first: one more round trip).
+    asm volatile("" ::"s"(src), "s"(src_stride), "s"(u_off), "s"(n_rows), "s"(n_max), "s"(cols), "s"(cols_pad),
+                 "s"(hi), "s"(lo), "s"(sc), "s"(q_stride), "s"(s_stride));
     const uint32_t nunit = cols_pad / 256;
-    const uint64_t unit = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint64_t unit = ((uint64_t)blockIdx.x * 256 + threadIdx.x) >> 6;  // 256 threads (launch_quantize*)
     const uint32_t rows = n_rows ? min(*n_rows, n_max) : n_max;
     if (unit >= (uint64_t)rows * nunit) return;  // whole wave exits together
     quantize_unit_wave<SILU>(src, src_stride, u_off, unit / nunit, (uint32_t)(unit % nunit), cols, hi, lo, sc, q_stride,

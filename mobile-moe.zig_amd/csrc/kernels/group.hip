@@ -446,6 +446,12 @@ __global__ __launch_bounds__((16 / KS) * KS * 64) void qmm_q8_fused_kernel(QmmQ8
     // Block b -> (item, tile group): the eight workgroups b = 8 r + x (one
     // per XCD) take tile groups 8 (r / items) + x of item r % items, so each
     // XCD's L2 holds one eighth of the matrix for every item.
+    // Every argument read at once (one batch of scalar loads, one wait;
+    // read where first used, the early exit below waited for its own loads
+    // first: a second kernel-argument round trip).
+    asm volatile("" ::"s"(a.recs), "s"(a.dvals), "s"(a.rec_stride), "s"(a.d_stride), "s"(a.d_row), "s"(a.x),
+                 "s"(a.x_stride), "s"(a.x_bytes), "s"(a.cols), "s"(a.y), "s"(a.y_slot), "s"(a.y_row), "s"(a.mat),
+                 "s"(a.batch), "s"(a.tiles), "s"(a.units), "s"(a.rows), "s"(a.tgroups));
     const uint32_t n_items = (a.batch + kGRows - 1) / kGRows;
     const uint32_t xcd = blockIdx.x & 7, r8 = blockIdx.x >> 3;
     const uint32_t item = r8 % n_items, tg = (r8 / n_items) * 8 + xcd;

@@ -197,11 +197,15 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
 }
 
 
-__global__ void combine_kernel(const float* __restrict__ eo, const int32_t* __restrict__ assign_slot,
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ eo, const int32_t* __restrict__ assign_slot,
                                const float* __restrict__ assign_w, const int32_t* __restrict__ shared_slot,
                                const uint32_t* __restrict__ deferred, const float* __restrict__ bias,
                                float* __restrict__ out, uint32_t n_tokens, uint32_t hidden) {
-    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // All arguments in one batch of scalar loads (the bounds check below
+    // otherwise waited for its own first: one more round trip).
+    asm volatile("" ::"s"(eo), "s"(assign_slot), "s"(assign_w), "s"(shared_slot), "s"(deferred), "s"(bias), "s"(out),
+                 "s"(n_tokens), "s"(hidden));
+    const uint64_t gid = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // 256 threads (launch_combine)
     if (gid >= (uint64_t)n_tokens * hidden) return;
     const uint32_t t = (uint32_t)(gid / hidden), j = (uint32_t)(gid % hidden);
     float o = 0.0f;
