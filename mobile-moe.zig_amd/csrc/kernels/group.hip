@@ -168,8 +168,9 @@ __device__ __forceinline__ void step_group_q8(const uint4 (&r)[kMaxUnitsPerStep]
 }
 
 // The launch bound's second argument is the minimum waves per SIMD: two
-// 512-thread IQ2_XXS workgroups share a CU (their LDS fits twice), four waves
-// per SIMD, so at most 128 registers.
+// 512-thread IQ2_XXS workgroups share a CU (their LDS fits twice), or one
+// 1024-thread workgroup fills it: four waves per SIMD either way, so at most
+// 128 registers.
 template <int FMT, int UPS, int WG>
 __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG >= 512) ? 4 : 2) void group_kernel(GroupArgs a) {
     constexpr uint32_t kWaves = WG / 64;
@@ -185,13 +186,14 @@ __global__ __launch_bounds__(WG, (FMT == kFmtIq2 && WG >= 512) ? 4 : 2) void gro
     // or partial tile runs of one or two items; the activations are staged
     // once per item run.
     //
-    // A range that crosses into a new item pays for the switch (the pipeline
+    // Grouped 1024-thread launches (a.gap > 0; the host sets it): a range
+    // that crosses into a new item pays for the switch (the pipeline
     // drains, then the item's work entry, rows, digits and first weights come
     // in series: ~5.5 steps per wave, s_memrealtime per workgroup), and the
     // workgroups that cross set the launch's end. So the ranges are cut
     // equally on a line where every item counts a.gap extra tiles after its
     // own: a crossing workgroup gets about a switch's worth fewer tiles.
-    // Virtual position v maps to item v / V, tile min(v % V, tiles): the
+    // Position v of that line is item v / vlen, tile min(v % vlen, tiles): the
     // map is monotone and onto, so the ranges still cover every (item, tile)
     // exactly once.
     const uint32_t n_items = a.work ? *a.n_work : (a.batch + kGRows - 1) / kGRows;
