@@ -163,6 +163,28 @@ __device__ __forceinline__ uint16_t buf_load_b16(BufRsrc r, uint32_t voff, uint3
     return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, POL);
 }
 
+// Problem p of a GEMV launch with an optional device problem list (probs:
+// {matrix, x row, y row, 0} per problem; n_active: its count): false when the
+// count leaves p out of this call. Without a list (both null) nothing is
+// read: the branch is uniform, so the first weight load waits for no vector
+// round trip. With one, the count and the entry load together and one wait
+// covers both (the asm needs both values before either is used; a null
+// pointer is a zero-size resource, whose load returns zeros).
+__device__ __forceinline__ bool read_problem(const uint4* probs, const uint32_t* n_active, uint32_t p, uint64_t& mat,
+                                             uint64_t& x_row, uint64_t& y_row) {
+    if (!probs && !n_active) return true;
+    uint32_t n_act = buf_load_b32(make_rsrc(n_active, n_active ? 4u : 0u), 0, 0);
+    uint4 d = buf_load_b128(make_rsrc(probs, probs ? (p + 1) * 16u : 0u), p * 16u, 0);
+    asm volatile("" : "+v"(n_act), "+v"(d.x), "+v"(d.y), "+v"(d.z));
+    if (n_active && p >= __builtin_amdgcn_readfirstlane(n_act)) return false;
+    if (probs) {
+        mat = __builtin_amdgcn_readfirstlane(d.x);
+        x_row = __builtin_amdgcn_readfirstlane(d.y);
+        y_row = __builtin_amdgcn_readfirstlane(d.z);
+    }
+    return true;
+}
+
 __device__ __forceinline__ v4i mfma_i8(long a, long b) {
     v4i z = {0, 0, 0, 0};
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);

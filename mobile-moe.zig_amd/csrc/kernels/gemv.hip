@@ -103,16 +103,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
             return;  // whole workgroup: no such problem this call
         }
     } else {
-        // The count and the problem's entry in one round trip (a null list
-        // is a zero-size resource: its load returns zeros, no access).
-        const uint32_t n_act = buf_load_b32(make_rsrc(a.n_active, a.n_active ? 4u : 0u), 0, 0);
-        const uint4 d = buf_load_b128(make_rsrc(a.probs, a.probs ? (p + 1) * 16u : 0u), p * 16u, 0);
-        if (a.n_active && p >= n_act) return;  // whole workgroup: problem not in this call's list
-        if (a.probs) {
-            mat = d.x;
-            x_row = d.y;
-            y_row = d.z;
-        }
+        if (!read_problem(a.probs, a.n_active, p, mat, x_row, y_row)) return;  // whole workgroup: not in this call
     }
     const float* x = a.x + x_row * a.x_stride;
     float* const y_base = a.y + y_row * a.y_stride;

@@ -93,17 +93,7 @@ __device__ __forceinline__ bool select_problem(const GemvArgs& a, uint32_t p, ui
         }
         return false;
     } else {
-        // The count and the problem's entry in one round trip (a null list
-        // is a zero-size resource: its load returns zeros, no access).
-        const uint32_t n_act = buf_load_b32(make_rsrc(a.n_active, a.n_active ? 4u : 0u), 0, 0);
-        const uint4 d = buf_load_b128(make_rsrc(a.probs, a.probs ? (p + 1) * 16u : 0u), p * 16u, 0);
-        if (a.n_active && p >= n_act) return false;
-        if (a.probs) {
-            mat = d.x;
-            x_row = d.y;
-            y_row = d.z;
-        }
-        return true;
+        return read_problem(a.probs, a.n_active, p, mat, x_row, y_row);
     }
 }
 
