@@ -2,18 +2,20 @@
 // inference.zig:1222-1226, and the expert products of expertFFN,
 // inference.zig:1171-1185, without the f32 dequantization round trip).
 //
-// One 1024-thread workgroup per CU owns one problem (matrix + activation
-// vector) and up to kQMaxTiles 16-row tiles (kQMaxItems record units per
-// activation chunk). A launch may hold several segments (weights of
-// different shapes), each one slice (blockIdx.z) of the grid. The activation is quantised into
+// A workgroup owns one problem (matrix + activation vector) and up to
+// IqShape::kMaxTiles 16-row tiles (kMaxItems record units per activation
+// chunk): two 768-thread workgroups per CU by default, or one of 1024 threads
+// (IqShape). A launch may hold several segments (weights of different
+// shapes), each one slice (blockIdx.z) of the grid. The activation is quantised into
 // LDS per K-chunk of up to 8 record units (2048 columns) as two int8 digit
 // planes per 32-column block (x ~ s (256 hi + lo)).
 //
-// Work items are (unit, tile) pairs in unit-major order, split into 16 equal
+// Work items are (unit, tile) pairs in unit-major order, split into equal
 // contiguous runs, one per wave, so a wave keeps one unit's activation
-// operands in registers while it walks tiles. The table reads of item i + 1
-// are issued before item i's arithmetic, so their latency overlaps it (two
-// sets of table words in registers). The A operands are sparse: for
+// operands in registers while it walks tiles. In the 1024-thread shape the
+// table reads of item i + 1 are issued before item i's arithmetic, so their
+// latency overlaps it (two sets of table words in registers); the 768-thread
+// shape hides it with its 24 waves per CU instead. The A operands are sparse: for
 // the 16x16x64 MFMA of blocks 2j, 2j + 1 (lane group g's K range carries
 // the record of sub-block 2j, then that of 2j + 1, both at columns
 // 8g..8g+7) only the lanes whose A row m = 4i + e belongs to one of those
@@ -28,9 +30,10 @@
 // layout in device_common.hpp); the hi3 signs of the high dword come from an
 // 8-entry mask table and are applied with one xor-add.
 //
-// Each item leaves its 64 lane partial sums in LDS; after a chunk, every
-// output row adds its (unit, lane group) partials in a fixed order, so the
-// result does not depend on timing.
+// Each item leaves its 64 lane partial sums in LDS (768 threads: the four
+// lane groups of each row summed in registers first, in the same order);
+// after a chunk, every output row adds its (unit, lane group) partials in a
+// fixed order, so the result does not depend on timing or on the shape.
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "route_ops.hpp"
@@ -40,19 +43,31 @@ namespace mmhip {
 
 namespace {
 
-constexpr int kQWg = 1024;
-constexpr uint32_t kQWaves = kQWg / 64;
 constexpr uint32_t kQChunkUnits = 8;                 // record units per activation chunk
 constexpr uint32_t kQChunkBlocks = kQChunkUnits * 8;  // 32-column blocks per chunk
-constexpr uint32_t kQMaxTiles = 64;                  // row tiles per workgroup
-constexpr uint32_t kQMaxItems = 384;                 // (unit, tile) items per workgroup and chunk
+
+// Workgroup shapes. 1024 threads: one workgroup per CU (16 waves), each
+// item's 64 lane partials kept in LDS. 768 threads: two workgroups per CU
+// (24 waves), which the CU holds only at <= 80 VGPRs and <= 52 KB of LDS per
+// workgroup, so an item's four lane groups are summed in registers (16 row
+// values per item in LDS) and the next item's table reads are not issued
+// ahead (one register set of table words).
+template <int WG>
+struct IqShape {
+    static constexpr bool kPair = WG == 768;
+    static constexpr uint32_t kWaves = WG / 64;
+    static constexpr uint32_t kMaxTiles = kPair ? 32 : 64;    // row tiles per workgroup
+    static constexpr uint32_t kMaxItems = kPair ? 192 : 384;  // (unit, tile) items per workgroup and chunk
+    static constexpr uint32_t kPartPerItem = kPair ? 16 : 64;
+};
 
 
 // Activation columns [c0, c0 + 32 nblk) of the problem's vector (times
-// silu(x) * u when silu_mul) into the digit planes; 128 blocks per pass.
+// silu(x) * u when silu_mul) into the digit planes; WG / 8 blocks per pass.
+template <int WG>
 __device__ __forceinline__ void quantize_planes(BufRsrc xr, BufRsrc ur, bool silu_mul, uint32_t nblk, uint8_t* aq,
                                                 float* xs) {
-    for (uint32_t b0 = 0; b0 < nblk; b0 += kQWg / 8) {
+    for (uint32_t b0 = 0; b0 < nblk; b0 += WG / 8) {
         float v[4], u[4];
         x_pass_load(xr, b0, v);
         x_pass_load(ur, b0, u);
@@ -104,21 +119,27 @@ struct ItemPos {
 };
 
 
-template <int DEPTH, bool ROUTE, int NSEG>
-__global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
+template <int DEPTH, bool ROUTE, int NSEG, int WG = 1024>
+__global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
+    using Shape = IqShape<WG>;
+    constexpr bool kPair = Shape::kPair;
+    constexpr uint32_t kWaves = Shape::kWaves;
     constexpr int kRing = DEPTH + 1;
-    static_assert(kRing % 2 == 0, "two table-word sets alternate over the ring");
+    static_assert(kPair || kRing % 2 == 0, "two table-word sets alternate over the ring");
     // One LDS block with the table first: its byte offsets (below 32 KiB)
     // fold into the ds_read offset fields.
     struct Lds {
         uint32_t tab[kIq2TableWords];
         uint32_t mtab[8];  // hi3 sign masks
-        alignas(16) float part[kQMaxItems * 64];  // per item: row n's lane groups g at 4 n + g
+        // Per item: row n's lane groups g at 4 n + g, or (kPair) row n's sum
+        // over its lane groups at n.
+        alignas(16) float part[Shape::kMaxItems * Shape::kPartPerItem];
         uint8_t aq[kQChunkBlocks * 64];
         float xs[kQChunkBlocks];
-        float row_sum[kQMaxTiles * 16];
+        float row_sum[Shape::kMaxTiles * 16];
         uint32_t sel[2];  // ROUTE: the routed problem's matrix (~0u: none) and output row
     };
+    static_assert(!kPair || sizeof(Lds) <= 52 * 1024, "two workgroups per CU need <= 52 KB of LDS each");
     __shared__ __align__(16) Lds lds;
     uint32_t* const tab = lds.tab;
     const uint32_t* const mtab = lds.mtab;
@@ -168,8 +189,8 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
         uc = units_in_chunk;
         tp_n = n_tiles;
         const uint32_t N = uc * tp_n;
-        p0 = wave * N / kQWaves;
-        p1 = (wave + 1) * N / kQWaves;
+        p0 = wave * N / kWaves;
+        p1 = (wave + 1) * N / kWaves;
     };
     auto advance = [&](ItemPos q) { return (q.t + 1 == tp_n) ? ItemPos{q.ul + 1, 0} : ItemPos{q.ul, q.t + 1}; };
     // Loads item q (ItemPos.t = tile within the range).
@@ -207,9 +228,10 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
         const BufRsrc x_r = make_rsrc(x, xb);
         const BufRsrc u_r = make_rsrc(x + a.x2_off, silu_mul ? xb : 0);  // zero-size: loads read 0
         const BufRsrc t_r = make_rsrc(&c_iq2_tables, sizeof(Iq2Tables));
-        uint4 tv[2];
+        constexpr uint32_t kTabVecs = kIq2TableWords / 4, kTabPer = (kTabVecs + WG - 1) / WG;
+        uint4 tv[kTabPer];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) tv[i] = buf_load_b128(t_r, (threadIdx.x + kQWg * i) * 16, 0);
+        for (uint32_t i = 0; i < kTabPer; ++i) tv[i] = buf_load_b128(t_r, (threadIdx.x + WG * i) * 16, 0);
         float xv[4], uv[4];
         x_pass_load(x_r, 0, xv);
         x_pass_load(u_r, 0, uv);
@@ -237,15 +259,18 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
         if constexpr (!ROUTE) __builtin_amdgcn_s_barrier();
         issue_first();
 #pragma unroll
-        for (int i = 0; i < 2; ++i) reinterpret_cast<uint4*>(tab)[threadIdx.x + kQWg * i] = tv[i];
+        for (uint32_t i = 0; i < kTabPer; ++i)
+            if (kTabVecs % WG == 0 || threadIdx.x + WG * i < kTabVecs)
+                reinterpret_cast<uint4*>(tab)[threadIdx.x + WG * i] = tv[i];
         if (threadIdx.x < 8) {
             // Columns 4..6 take hi3's bits, column 7 its parity (the ksigns
             // parity bit; column 7's P sign is already in the table word).
             lds.mtab[threadIdx.x] = iq2_hi3_mask(threadIdx.x);
         }
-        for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += kQWg) row_sum[i] = 0.0f;
+        for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) row_sum[i] = 0.0f;
         if (silu_mul) silu_mul4(xv, uv);
-        x_store_planes(xv, nb, 0, aq, xs);  // one pass covers 128 >= 64 blocks
+        static_assert(WG / 8 >= kQChunkBlocks, "one pass quantises the first chunk");
+        x_store_planes(xv, nb, 0, aq, xs);
     }
 
     for (uint32_t kc = 0;;) {
@@ -253,69 +278,103 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
         v4i av[4];
         float xa = 0.0f, xb = 0.0f, ha = 0.0f, hb = 0.0f;
         uint32_t a_ul = 0xFFFFFFFFu;
-        // Single items; the table reads of item i + 1 are issued before item
-        // i's arithmetic (two register sets, kRing even keeps the set of an
-        // item fixed at compile time).
-        RawB raw[2];
-        if (p0 < p1) fetch_b(rb[0], tab, mtab, raw[0]);
-        for (uint32_t i = p0; i < p1; i += kRing) {
-            // Issue priority by items left, set once per kRing items: the
-            // hardware otherwise favours a SIMD's oldest wave, whose items
-            // then finish far ahead of the youngest's, and the workgroup
-            // waits for the last wave with the CU part idle.
-            const uint32_t rem = p1 - i;
+        // This unit's sparse A operands and block scales.
+        auto set_unit = [&](uint32_t ul) {
+            a_ul = ul;
+            const uint8_t* ap = aq + ((a_ul * 8 + s_star) * 2 + d_star) * 32 + 8 * g;
+            const uint2 xw = *reinterpret_cast<const uint2*>(ap);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool lo = s_star == 2u * j, hi = s_star == 2u * j + 1;
+                av[j] = v4i{(int)(lo ? xw.x : 0u), (int)(lo ? xw.y : 0u), (int)(hi ? xw.x : 0u), (int)(hi ? xw.y : 0u)};
+            }
+            xa = xs[a_ul * 8 + g] * 0.25f;
+            xb = xs[a_ul * 8 + g + 4] * 0.25f;
+            ha = xa * 0.5f;
+            hb = xb * 0.5f;
+        };
+        // Lane (g, n)'s partial of row n for the item in ring slot q, whose
+        // table words (signs applied) are b.
+        auto item_value = [&](const RawB& b, int q) {
+            v4i acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], b.e[j], acc, 0, 0, 0);
+            // Blocks g and g + 4 of row n: d * (0.5 + ls) / 4 * s_x * digits.
+            const uint4& r = rb[q];
+            const float df = f16_scale(db[q]);
+            const float sa = fmaf((float)iq2_ls_a(r), xa, ha);
+            const float sb = fmaf((float)iq2_ls_b(r), xb, hb);
+            float v = (float)digits_combine(acc[0], acc[1]) * sa;
+            v = fmaf((float)digits_combine(acc[2], acc[3]), sb, v);
+            return v * df;
+        };
+        // Issue priority by items left, set once per kRing items: the
+        // hardware otherwise favours a SIMD's oldest wave, whose items then
+        // finish far ahead of the youngest's, and the workgroup waits for the
+        // last wave with the CU part idle.
+        auto set_priority = [&](uint32_t rem) {
             if (rem > 8) __builtin_amdgcn_s_setprio(3);
             else if (rem > 4) __builtin_amdgcn_s_setprio(2);
             else if (rem > 2) __builtin_amdgcn_s_setprio(1);
             else __builtin_amdgcn_s_setprio(0);
+        };
+        if constexpr (kPair) {
+            // Single items, table reads after the item's record arrives (one
+            // register set); an item's lane groups summed in registers.
+            for (uint32_t i = p0; i < p1; i += kRing) {
+                set_priority(p1 - i);
 #pragma unroll
-            for (int q = 0; q < kRing; ++q) {
-                if (i + q < p1) {
-                    load(i + q + DEPTH < p1, nxt, rb[(q + DEPTH) % kRing], db[(q + DEPTH) % kRing]);
-                    nxt = advance(nxt);
-                    if (i + q + 1 < p1) fetch_b(rb[(q + 1) % kRing], tab, mtab, raw[(q + 1) & 1]);
-                    if (cur.ul != a_ul) {
-                        // This unit's sparse A operands and block scales.
-                        a_ul = cur.ul;
-                        const uint8_t* ap = aq + ((a_ul * 8 + s_star) * 2 + d_star) * 32 + 8 * g;
-                        const uint2 xw = *reinterpret_cast<const uint2*>(ap);
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const bool lo = s_star == 2u * j, hi = s_star == 2u * j + 1;
-                            av[j] = v4i{(int)(lo ? xw.x : 0u), (int)(lo ? xw.y : 0u), (int)(hi ? xw.x : 0u),
-                                        (int)(hi ? xw.y : 0u)};
-                        }
-                        xa = xs[a_ul * 8 + g] * 0.25f;
-                        xb = xs[a_ul * 8 + g + 4] * 0.25f;
-                        ha = xa * 0.5f;
-                        hb = xb * 0.5f;
+                for (int q = 0; q < kRing; ++q) {
+                    if (i + q < p1) {
+                        load(i + q + DEPTH < p1, nxt, rb[(q + DEPTH) % kRing], db[(q + DEPTH) % kRing]);
+                        nxt = advance(nxt);
+                        RawB raw;
+                        fetch_b(rb[q], tab, mtab, raw);
+                        if (cur.ul != a_ul) set_unit(cur.ul);
+                        finish_b(raw);
+                        const float rv = item_rows(item_value(raw, q));
+                        if (lane < 16) part[(cur.ul * n_tiles + cur.t) * 16 + n] = rv;
+                        cur = advance(cur);
                     }
-                    finish_b(raw[q & 1]);
-                    v4i acc = {0, 0, 0, 0};
+                }
+            }
+        } else {
+            // Single items; the table reads of item i + 1 are issued before
+            // item i's arithmetic (two register sets, kRing even keeps the
+            // set of an item fixed at compile time).
+            RawB raw[2];
+            if (p0 < p1) fetch_b(rb[0], tab, mtab, raw[0]);
+            for (uint32_t i = p0; i < p1; i += kRing) {
+                set_priority(p1 - i);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[j], raw[q & 1].e[j], acc, 0, 0, 0);
-                    // Blocks g and g + 4 of row n: d * (0.5 + ls) / 4 * s_x * digits.
-                    const uint4& r = rb[q];
-                    const float df = f16_scale(db[q]);
-                    const float sa = fmaf((float)iq2_ls_a(r), xa, ha);
-                    const float sb = fmaf((float)iq2_ls_b(r), xb, hb);
-                    float v = (float)digits_combine(acc[0], acc[1]) * sa;
-                    v = fmaf((float)digits_combine(acc[2], acc[3]), sb, v);
-                    part[(cur.ul * n_tiles + cur.t) * 64 + part_slot] = v * df;
-                    cur = advance(cur);
+                for (int q = 0; q < kRing; ++q) {
+                    if (i + q < p1) {
+                        load(i + q + DEPTH < p1, nxt, rb[(q + DEPTH) % kRing], db[(q + DEPTH) % kRing]);
+                        nxt = advance(nxt);
+                        if (i + q + 1 < p1) fetch_b(rb[(q + 1) % kRing], tab, mtab, raw[(q + 1) & 1]);
+                        if (cur.ul != a_ul) set_unit(cur.ul);
+                        finish_b(raw[q & 1]);
+                        part[(cur.ul * n_tiles + cur.t) * 64 + part_slot] = item_value(raw[q & 1], q);
+                        cur = advance(cur);
+                    }
                 }
             }
         }
         lds_barrier();  // every item's partials written
         // Row sums: units in order, lane groups in order (one 16-byte read
-        // per unit; a wave's lanes read consecutive words, no bank conflicts).
-        for (uint32_t idx = threadIdx.x; idx < n_tiles * 16; idx += kQWg) {
+        // per unit, or the unit's row value already summed over its lane
+        // groups in that order; a wave's lanes read consecutive words, no
+        // bank conflicts).
+        for (uint32_t idx = threadIdx.x; idx < n_tiles * 16; idx += WG) {
             const uint32_t t = idx >> 4, rr = idx & 15;
             float sum = 0.0f;
             for (uint32_t ul = 0; ul < uc; ++ul) {
-                const float4 q = *reinterpret_cast<const float4*>(part + (ul * n_tiles + t) * 64 + rr * 4);
-                sum += ((q.x + q.y) + q.z) + q.w;
+                if constexpr (kPair) {
+                    sum += part[(ul * n_tiles + t) * 16 + rr];
+                } else {
+                    const float4 q = *reinterpret_cast<const float4*>(part + (ul * n_tiles + t) * 64 + rr * 4);
+                    sum += ((q.x + q.y) + q.z) + q.w;
+                }
             }
             row_sum[idx] += sum;
         }
@@ -327,13 +386,13 @@ __global__ __launch_bounds__(kQWg, 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
         const uint32_t ucn = min(a.units - kc, kQChunkUnits);
         const uint32_t c0 = kc * 256;
         const uint32_t cb = (a.cols > c0 ? min(a.cols - c0, ucn * 256) : 0) * 4;
-        quantize_planes(make_rsrc(x + c0, cb), make_rsrc(x + a.x2_off + c0, silu_mul ? cb : 0), silu_mul, ucn * 8,
+        quantize_planes<WG>(make_rsrc(x + c0, cb), make_rsrc(x + a.x2_off + c0, silu_mul ? cb : 0), silu_mul, ucn * 8,
                         aq, xs);
         start_chunk(kc, ucn);
         issue_first();
     }
     lds_barrier();  // all row sums final
-    for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += kQWg) {
+    for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) {
         const uint32_t row = (t_begin + (i >> 4)) * 16 + (i & 15);
         if (row < a.rows) y_base[row] = row_sum[i];
     }
@@ -344,12 +403,13 @@ static int env_int(const char* name, int dflt) {
     return e ? atoi(e) : dflt;
 }
 
-// Largest tiles per workgroup for a segment: the LDS holds kQMaxTiles row
-// sums and kQMaxItems (unit, tile) partials per activation chunk.
+// Largest tiles per workgroup for a segment: the LDS holds kMaxTiles row
+// sums and kMaxItems (unit, tile) partials per activation chunk.
+template <int WG>
 static uint32_t max_tiles_per_wg(const GemvArgs& a) {
     const uint32_t uc = a.units < kQChunkUnits ? a.units : kQChunkUnits;
-    uint32_t m = kQMaxItems / uc;
-    if (m > kQMaxTiles) m = kQMaxTiles;
+    uint32_t m = IqShape<WG>::kMaxItems / uc;
+    if (m > IqShape<WG>::kMaxTiles) m = IqShape<WG>::kMaxTiles;
     return a.tiles < m ? a.tiles : m;
 }
 
@@ -526,7 +586,8 @@ __global__ __launch_bounds__(kDcWg, 1) void down_combine_iq2_kernel(DownCombineA
 }
 
 template <int N>
-static hipError_t launch_set(const GemvArgs* segs, uint32_t n_segs, const void* fn, uint32_t grid_x, hipStream_t s) {
+static hipError_t launch_set(const GemvArgs* segs, uint32_t n_segs, const void* fn, uint32_t grid_x, uint32_t wg,
+                             hipStream_t s) {
     GemvSet<N> set{};
     uint32_t y = 0;
     for (uint32_t i = 0; i < (uint32_t)N; ++i) {
@@ -534,7 +595,55 @@ static hipError_t launch_set(const GemvArgs* segs, uint32_t n_segs, const void* 
         if (i < n_segs && segs[i].n_probs > y) y = segs[i].n_probs;
     }
     void* args[] = {&set};
-    return hipLaunchKernel(fn, dim3(grid_x, y, n_segs), dim3(kQWg), args, 0, s);
+    return hipLaunchKernel(fn, dim3(grid_x, y, n_segs), dim3(wg), args, 0, s);
+}
+
+// Tiles per workgroup of every segment and the grid's x extent for W
+// workgroups of shape WG, `slots` of which fit the GPU at once.
+template <int WG>
+static uint32_t plan_tiles(GemvArgs* segs, uint32_t n, uint64_t slots) {
+    uint32_t grid_x = 1;
+    if (n == 1) {
+        // Tiles per workgroup. A grid of W workgroups runs in
+        // ceil(W / slots) rounds; the choice minimises rounds x (tiles x
+        // units x per-item time + per-workgroup fixed time), with the costs
+        // measured on MI355X for one 1024-thread workgroup per CU (~65 ns per
+        // 1 KiB item per CU, ~2 us of prologue and tail). E.g. 10 matrices
+        // of 128 tiles take 6 tiles per workgroup (220 workgroups, one round)
+        // rather than 5 (260, two rounds).
+        GemvArgs& a = segs[0];
+        const uint32_t max_tpw = max_tiles_per_wg<WG>(a);
+        uint32_t tpw = max_tpw;
+        double best = 0.0;
+        for (uint32_t t = 1; t <= max_tpw; ++t) {
+            const uint64_t wgs = (uint64_t)a.n_probs * ((a.tiles + t - 1) / t);
+            const double cost = (double)((wgs + slots - 1) / slots) * ((double)t * a.units * 0.065 + 2.0);
+            if (t == 1 || cost < best) {
+                best = cost;
+                tpw = t;
+            }
+        }
+        a.tiles_per_wg = tpw;
+        grid_x = (a.tiles + tpw - 1) / tpw;
+    } else {
+        // Several segments: every workgroup gets about the same number of
+        // items (the total over the slots), so the whole launch is one round
+        // when the segments allow it.
+        uint64_t items = 0;
+        for (uint32_t i = 0; i < n; ++i) items += (uint64_t)segs[i].n_probs * segs[i].tiles * segs[i].units;
+        const uint64_t per_wg = (items + slots - 1) / slots;
+        for (uint32_t i = 0; i < n; ++i) {
+            GemvArgs& a = segs[i];
+            uint64_t t = (per_wg + a.units - 1) / a.units;
+            const uint32_t m = max_tiles_per_wg<WG>(a);
+            if (t > m) t = m;
+            if (t < 1) t = 1;
+            a.tiles_per_wg = (uint32_t)t;
+            const uint32_t gx = (a.tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
+            if (gx > grid_x) grid_x = gx;
+        }
+    }
+    return grid_x;
 }
 
 }  // namespace
@@ -549,60 +658,33 @@ hipError_t launch_gemv_iq2(const GemvArgs* segs_in, uint32_t n_segs, int num_cu,
     const bool route = segs[0].route_decode != 0;
     if (route && n != 1) return hipErrorInvalidValue;
     const uint64_t cus = (uint64_t)(num_cu > 0 ? num_cu : 256);
-    uint32_t grid_x = 1;
-    if (n == 1) {
-        // Tiles per workgroup. One workgroup fits a CU, so a grid of W
-        // workgroups runs in ceil(W / CUs) rounds; the choice minimises
-        // rounds x (tiles x units x per-item time + per-workgroup fixed
-        // time), with the costs measured on MI355X (~65 ns per 1 KiB item
-        // per CU, ~2 us of prologue and tail). E.g. 10 matrices of 128 tiles
-        // take 6 tiles per workgroup (220 workgroups, one round) rather than
-        // 5 (260, two rounds).
-        GemvArgs& a = segs[0];
-        const uint32_t max_tpw = max_tiles_per_wg(a);
-        uint32_t tpw = max_tpw;
-        double best = 0.0;
-        for (uint32_t t = 1; t <= max_tpw; ++t) {
-            const uint64_t wgs = (uint64_t)a.n_probs * ((a.tiles + t - 1) / t);
-            const double cost = (double)((wgs + cus - 1) / cus) * ((double)t * a.units * 0.065 + 2.0);
-            if (t == 1 || cost < best) {
-                best = cost;
-                tpw = t;
-            }
-        }
-        a.tiles_per_wg = tpw;
-        grid_x = (a.tiles + tpw - 1) / tpw;
-    } else {
-        // Several segments: every workgroup gets about the same number of
-        // items (the total over the CUs), so the whole launch is one round
-        // when the segments allow it.
-        uint64_t items = 0;
-        for (uint32_t i = 0; i < n; ++i) items += (uint64_t)segs[i].n_probs * segs[i].tiles * segs[i].units;
-        const uint64_t per_wg = (items + cus - 1) / cus;
-        for (uint32_t i = 0; i < n; ++i) {
-            GemvArgs& a = segs[i];
-            uint64_t t = (per_wg + a.units - 1) / a.units;
-            const uint32_t m = max_tiles_per_wg(a);
-            if (t > m) t = m;
-            if (t < 1) t = 1;
-            a.tiles_per_wg = (uint32_t)t;
-            const uint32_t gx = (a.tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
-            if (gx > grid_x) grid_x = gx;
-        }
+    // Two 768-thread workgroups per CU, or one of 1024 (MMHIP_IQ2_PAIR=0).
+    static const int pair_env = env_int("MMHIP_IQ2_PAIR", 1);
+    if (pair_env != 0) {
+        const uint32_t grid_x = plan_tiles<768>(segs, n, 2 * cus);
+        const void* fn = route    ? reinterpret_cast<const void*>(&gemv_iq2_kernel<2, true, 1, 768>)
+                         : n == 1 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 1, 768>)
+                         : n == 2 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 2, 768>)
+                                  : reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 4, 768>);
+        if (n == 1) return launch_set<1>(segs, 1, fn, grid_x, 768, s);
+        if (n == 2) return launch_set<2>(segs, 2, fn, grid_x, 768, s);
+        return launch_set<4>(segs, n, fn, grid_x, 768, s);
     }
+    const uint32_t grid_x = plan_tiles<1024>(segs, n, cus);
     // Items in flight per wave: 3 (the ring of record buffers is 4, even so
     // that an item's table-word set is fixed at compile time); MMHIP_IQ2_DEPTH=5
     // to override.
     static const int depth_env = env_int("MMHIP_IQ2_DEPTH", 0);
-    if (route) return launch_set<1>(segs, 1, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, true, 1>), grid_x, s);
+    if (route)
+        return launch_set<1>(segs, 1, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, true, 1>), grid_x, 1024, s);
     if (n == 1) {
         const void* fn = depth_env == 5 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<5, false, 1>)
                                         : reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 1>);
-        return launch_set<1>(segs, 1, fn, grid_x, s);
+        return launch_set<1>(segs, 1, fn, grid_x, 1024, s);
     }
     if (n == 2)
-        return launch_set<2>(segs, 2, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 2>), grid_x, s);
-    return launch_set<4>(segs, n, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 4>), grid_x, s);
+        return launch_set<2>(segs, 2, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 2>), grid_x, 1024, s);
+    return launch_set<4>(segs, n, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 4>), grid_x, 1024, s);
 }
 
 hipError_t launch_down_combine_iq2(const DownCombineArgs& a, hipStream_t s) {
