@@ -659,13 +659,18 @@ hipError_t launch_gemv_iq2(const GemvArgs* segs_in, uint32_t n_segs, int num_cu,
     if (route && n != 1) return hipErrorInvalidValue;
     const uint64_t cus = (uint64_t)(num_cu > 0 ? num_cu : 256);
     // Two 768-thread workgroups per CU, or one of 1024 (MMHIP_IQ2_PAIR=0).
+    // The 768-thread shape keeps one record load in flight per wave while
+    // it computes another: with 24 waves per CU that is enough, and the
+    // headline 64 + 64 matrix step ran ~0.5 us faster than with two (the
+    // CU returns loads in issue order, so deeper prefetch only lengthens the
+    // queue in front of the record a wave needs next).
     static const int pair_env = env_int("MMHIP_IQ2_PAIR", 1);
     if (pair_env != 0) {
         const uint32_t grid_x = plan_tiles<768>(segs, n, 2 * cus);
-        const void* fn = route    ? reinterpret_cast<const void*>(&gemv_iq2_kernel<2, true, 1, 768>)
-                         : n == 1 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 1, 768>)
-                         : n == 2 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 2, 768>)
-                                  : reinterpret_cast<const void*>(&gemv_iq2_kernel<2, false, 4, 768>);
+        const void* fn = route    ? reinterpret_cast<const void*>(&gemv_iq2_kernel<1, true, 1, 768>)
+                         : n == 1 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<1, false, 1, 768>)
+                         : n == 2 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<1, false, 2, 768>)
+                                  : reinterpret_cast<const void*>(&gemv_iq2_kernel<1, false, 4, 768>);
         if (n == 1) return launch_set<1>(segs, 1, fn, grid_x, 768, s);
         if (n == 2) return launch_set<2>(segs, 2, fn, grid_x, 768, s);
         return launch_set<4>(segs, n, fn, grid_x, 768, s);
