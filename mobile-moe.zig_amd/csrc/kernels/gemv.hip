@@ -493,7 +493,8 @@ hipError_t launch_gemv_segments(const GemvArgs* segs_in, uint32_t n_segs, uint32
     // workgroup per CU, two steps of 4 units in flight: four long streams
     // per CU keep fewer requests outstanding and reach a higher HBM rate than
     // sixteen. Overrides: MMHIP_GEMV_WG (256 | 1024), MMHIP_GEMV_MAX_UPS (4 |
-    // 8 record units per step), MMHIP_GEMV_DEPTH (steps in flight, 1..3).
+    // 8 record units per step), MMHIP_GEMV_DEPTH (steps in flight, 1..3;
+    // default below).
     static const int wg_env = env_int("MMHIP_GEMV_WG", 0);
     static const int cap_env = env_int("MMHIP_GEMV_MAX_UPS", 0);
     static const int depth_env = env_int("MMHIP_GEMV_DEPTH", 0);
@@ -538,7 +539,12 @@ hipError_t launch_gemv_segments(const GemvArgs* segs_in, uint32_t n_segs, uint32
             if (gx > grid_x) grid_x = gx;
         }
     }
-    const int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : 2;
+    // One step in flight when every workgroup has a single tile (one matrix
+    // of at most a tile per CU: the MLA projections, a [1536 x 2048] call):
+    // such a call is bound by its first weight round trip, and a second
+    // step's loads only queue in front of the first one's (MLA Q8_0 decode
+    // 19.9 -> 19.2 us per layer). Larger launches keep two (HBM-bound).
+    const int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : (n == 1 && segs[0].tiles_per_wg == 1 ? 1 : 2);
     if (route) return launch_q_set<1>(segs, 1, kernel_for<256, 2, true, 1>(ups), grid_x, 256, lds, s);
     if (n == 1) {
         const void* fn =
