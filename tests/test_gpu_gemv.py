@@ -409,3 +409,54 @@ def test_headline_step_shape_matches_oracle(ctx, orc, t):
     finally:
         for a in (wg, wd, dx, dxd, yg, yd, yg1, yd1):
             a.free()
+
+
+_SHAPE_CHILD = r'''
+import sys
+import numpy as np
+import mmhip as mm
+out = sys.argv[1]
+ctx = mm.Context(0)
+rng = np.random.default_rng(880)
+res = {}
+# Two segments in one launch (a shared x, one x per matrix), as the decode step runs them.
+g_raw = mm.make_weight(rng, mm.IQ2_XXS, 1536, 2048, 6)
+d_raw = mm.make_weight(rng, mm.IQ2_XXS, 2048, 1536, 6)
+gw, dw = ctx.upload(g_raw, mm.IQ2_XXS, 1536, 2048, 6), ctx.upload(d_raw, mm.IQ2_XXS, 2048, 1536, 6)
+x = mm.DeviceArray.from_numpy(ctx, rng.standard_normal(2048).astype(np.float32))
+xd = mm.DeviceArray.from_numpy(ctx, rng.standard_normal((6, 1536)).astype(np.float32))
+yg, yd = mm.DeviceArray(ctx, 6 * 1536 * 4), mm.DeviceArray(ctx, 6 * 2048 * 4)
+ctx.gemv_grouped_dev([(gw, 0, 6, x, 0, yg, 1536), (dw, 0, 6, xd, 1536, yd, 2048)])
+ctx.synchronize()
+res["gate"], res["down"] = yg.to_numpy(np.float32, 6 * 1536), yd.to_numpy(np.float32, 6 * 2048)
+# One matrix per call: a single tile per workgroup, and a K of several activation chunks.
+for name, rows, cols in (("one", 2048, 1536), ("wide", 100, 5120)):
+    raw = mm.make_weight(rng, mm.IQ2_XXS, rows, cols)
+    res[name] = ctx.mat_vec_mul(raw, mm.IQ2_XXS, rng.standard_normal(cols).astype(np.float32), rows, cols)
+np.savez(out, **res)
+'''
+
+
+def test_iq2_workgroup_shapes_give_the_same_bits(tmp_path):
+    """The IQ2_XXS decode GEMV's two workgroup shapes (two 768-thread
+    workgroups per CU, the default, and one 1024-thread workgroup,
+    MMHIP_IQ2_PAIR=0) sum every row in the same order, so they must give the
+    same bits. The shape is chosen once per process, so each runs in a child
+    process on the same seeded inputs."""
+    import os
+    import subprocess
+    import sys
+    env_base = dict(os.environ)
+    env_base["PYTHONPATH"] = os.pathsep.join([os.path.dirname(mm.__file__), env_base.get("PYTHONPATH", "")])
+    outs = {}
+    for pair in ("1", "0"):
+        env = dict(env_base, MMHIP_IQ2_PAIR=pair)
+        out = tmp_path / f"shape_{pair}.npz"
+        r = subprocess.run([sys.executable, "-c", _SHAPE_CHILD, str(out)], env=env, capture_output=True, text=True,
+                           timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        outs[pair] = np.load(out)
+    for k in ("gate", "down", "one", "wide"):
+        a, b = outs["1"][k], outs["0"][k]
+        assert a.shape == b.shape and np.all(np.isfinite(a))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), k
