@@ -136,17 +136,18 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
         alignas(16) float part[Shape::kMaxItems * Shape::kPartPerItem];
         uint8_t aq[kQChunkBlocks * 64];
         float xs[kQChunkBlocks];
-        float row_sum[Shape::kMaxTiles * 16];
         uint32_t sel[2];  // ROUTE: the routed problem's matrix (~0u: none) and output row
     };
     static_assert(!kPair || sizeof(Lds) <= 52 * 1024, "two workgroups per CU need <= 52 KB of LDS each");
+    // Thread i owns output row i of the workgroup's range: its sum over the
+    // activation chunks stays in a register.
+    static_assert(Shape::kMaxTiles * 16 <= WG, "one output row per thread");
     __shared__ __align__(16) Lds lds;
     uint32_t* const tab = lds.tab;
     const uint32_t* const mtab = lds.mtab;
     float* const part = lds.part;
     uint8_t* const aq = lds.aq;
     float* const xs = lds.xs;
-    float* const row_sum = lds.row_sum;
 
     // This workgroup's segment (grid slice z) and problem within it (row y).
     const GemvArgs& a = set.seg[NSEG > 1 ? blockIdx.z : 0];
@@ -267,14 +268,14 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
             // parity bit; column 7's P sign is already in the table word).
             lds.mtab[threadIdx.x] = iq2_hi3_mask(threadIdx.x);
         }
-        for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) row_sum[i] = 0.0f;
         if (silu_mul) silu_mul4(xv, uv);
         static_assert(WG / 8 >= kQChunkBlocks, "one pass quantises the first chunk");
         x_store_planes(xv, nb, 0, aq, xs);
     }
 
+    float row_acc = 0.0f;  // this thread's output row, summed over the chunks
     for (uint32_t kc = 0;;) {
-        lds_barrier();  // tables, digit planes, scales (and row sums) visible
+        lds_barrier();  // tables, digit planes and scales visible
         v4i av[4];
         float xa = 0.0f, xb = 0.0f, ha = 0.0f, hb = 0.0f;
         uint32_t a_ul = 0xFFFFFFFFu;
@@ -365,8 +366,8 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
         // per unit, or the unit's row value already summed over its lane
         // groups in that order; a wave's lanes read consecutive words, no
         // bank conflicts).
-        for (uint32_t idx = threadIdx.x; idx < n_tiles * 16; idx += WG) {
-            const uint32_t t = idx >> 4, rr = idx & 15;
+        if (threadIdx.x < n_tiles * 16) {
+            const uint32_t t = threadIdx.x >> 4, rr = threadIdx.x & 15;
             float sum = 0.0f;
             for (uint32_t ul = 0; ul < uc; ++ul) {
                 if constexpr (kPair) {
@@ -376,7 +377,7 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
                     sum += ((q.x + q.y) + q.z) + q.w;
                 }
             }
-            row_sum[idx] += sum;
+            row_acc += sum;
         }
         kc += uc;
         if (kc >= a.units) break;
@@ -391,10 +392,9 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
         start_chunk(kc, ucn);
         issue_first();
     }
-    lds_barrier();  // all row sums final
-    for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) {
-        const uint32_t row = (t_begin + (i >> 4)) * 16 + (i & 15);
-        if (row < a.rows) y_base[row] = row_sum[i];
+    if (threadIdx.x < n_tiles * 16) {
+        const uint32_t row = (t_begin + (threadIdx.x >> 4)) * 16 + (threadIdx.x & 15);
+        if (row < a.rows) y_base[row] = row_acc;
     }
 }
 
@@ -677,19 +677,14 @@ hipError_t launch_gemv_iq2(const GemvArgs* segs_in, uint32_t n_segs, int num_cu,
     }
     const uint32_t grid_x = plan_tiles<1024>(segs, n, cus);
     // Items in flight per wave: 3 (the ring of record buffers is 4, even so
-    // that an item's table-word set is fixed at compile time); MMHIP_IQ2_DEPTH=5
-    // to override.
-    static const int depth_env = env_int("MMHIP_IQ2_DEPTH", 0);
-    if (route)
-        return launch_set<1>(segs, 1, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, true, 1>), grid_x, 1024, s);
-    if (n == 1) {
-        const void* fn = depth_env == 5 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<5, false, 1>)
-                                        : reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 1>);
-        return launch_set<1>(segs, 1, fn, grid_x, 1024, s);
-    }
-    if (n == 2)
-        return launch_set<2>(segs, 2, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 2>), grid_x, 1024, s);
-    return launch_set<4>(segs, n, reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 4>), grid_x, 1024, s);
+    // that an item's table-word set is fixed at compile time).
+    const void* fn = route    ? reinterpret_cast<const void*>(&gemv_iq2_kernel<3, true, 1>)
+                     : n == 1 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 1>)
+                     : n == 2 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 2>)
+                              : reinterpret_cast<const void*>(&gemv_iq2_kernel<3, false, 4>);
+    if (n == 1) return launch_set<1>(segs, 1, fn, grid_x, 1024, s);
+    if (n == 2) return launch_set<2>(segs, 2, fn, grid_x, 1024, s);
+    return launch_set<4>(segs, n, fn, grid_x, 1024, s);
 }
 
 hipError_t launch_down_combine_iq2(const DownCombineArgs& a, hipStream_t s) {
