@@ -219,11 +219,15 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
             }
         }
         lds_barrier();  // edge slots and whole-tile sums of this chunk written
-        // Split tiles: their pieces in wave order.
+        // Split tiles: their pieces in wave order. After the last chunk
+        // thread i stores row i itself: every other contribution to it was
+        // written before the barrier above.
+        const bool last = kb + chunk_blk >= nblk_all;
         for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) {
             const uint32_t t = i >> 4, rr = i & 15;
             const uint32_t w_first = ((t * S + 1) * kWaves - 1) / L;
             const uint32_t w_last = ((t * S + S) * kWaves - 1) / L;
+            float v = row_sum[i];
             if (w_first != w_last) {
                 float sum = 0.0f;
                 for (uint32_t w = w_first; w <= w_last; ++w) {
@@ -231,11 +235,16 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
                     if (aw == bw) continue;  // empty run
                     sum += edge[aw / S == t ? 0 : 1][w * 16 + rr];
                 }
-                row_sum[i] += sum;
+                v += sum;
+                if (!last) row_sum[i] = v;
+            }
+            if (last) {
+                const uint32_t row = (t_begin + t) * 16 + rr;
+                if (row < a.rows) y_base[row] = v;
             }
         }
+        if (last) break;
         kb += chunk_blk;
-        if (kb >= nblk_all) break;
         // Next K-chunk (activations longer than one LDS chunk).
         const uint32_t nb = min(chunk_blk, nblk_all - kb);
         lds_barrier();  // previous chunk's LDS (activations, edge slots) no longer in use
@@ -246,11 +255,6 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
                             xs);
         start_chunk(nb);
         issue_first();
-    }
-    lds_barrier();  // all row sums final
-    for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) {
-        const uint32_t row = (t_begin + (i >> 4)) * 16 + (i & 15);
-        if (row < a.rows) y_base[row] = row_sum[i];
     }
 }
 
