@@ -179,22 +179,35 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
         const uint32_t xb = min(a.cols, chunk_blk * 32) * 4;
         const BufRsrc x_r = make_rsrc(x, xb);
         const BufRsrc u_r = make_rsrc(x + a.x2_off, silu_mul ? xb : 0);  // zero-size: loads read 0
-        float xv[4], uv[4];
-        x_pass_load(x_r, 0, xv);
-        x_pass_load(u_r, 0, uv);
+        // The activation passes of the first 96 blocks (3072 columns) load
+        // before the weights: one workgroup per CU leaves registers to spare.
+        constexpr uint32_t kPass = WG / 8, kPre = (96 + kPass - 1) / kPass;
+        float xv[kPre][4], uv[kPre][4];
+#pragma unroll
+        for (uint32_t q = 0; q < kPre; ++q) {
+            if (q == 0 || q * kPass < nb) {
+                x_pass_load(x_r, q * kPass, xv[q]);
+                x_pass_load(u_r, q * kPass, uv[q]);
+            }
+        }
         // The first weight steps go out now, behind every wave's activation
         // loads (the barrier orders the issue; the CU returns
         // loads in issue order), so their HBM latency overlaps the prologue's
         // loads and the LDS fill below; the waits for the prologue data leave
-        // them in flight. Activation passes beyond the first (chunks wider
-        // than WG / 8 blocks) return behind them.
+        // them in flight. Activation passes beyond kPre (chunks wider than
+        // 96 blocks) return behind them.
         start_chunk(nb);
         __builtin_amdgcn_s_barrier();
         issue_first();
         for (uint32_t i = threadIdx.x; i < n_tiles * 16; i += WG) row_sum[i] = 0.0f;
-        if (silu_mul) silu_mul4(xv, uv);
-        x_pass_store(xv, nb, 0, aq, xs);
-        for (uint32_t b0 = WG / 8; b0 < nb; b0 += WG / 8) {
+#pragma unroll
+        for (uint32_t q = 0; q < kPre; ++q) {
+            if (q == 0 || q * kPass < nb) {
+                if (silu_mul) silu_mul4(xv[q], uv[q]);
+                x_pass_store(xv[q], nb, q * kPass, aq, xs);
+            }
+        }
+        for (uint32_t b0 = kPre * kPass; b0 < nb; b0 += kPass) {
             float v[4], u[4];
             x_pass_load(x_r, b0, v);
             x_pass_load(u_r, b0, u);
