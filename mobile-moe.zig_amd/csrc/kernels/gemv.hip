@@ -556,12 +556,15 @@ hipError_t launch_gemv_segments(const GemvArgs* segs_in, uint32_t n_segs, uint32
             if (gx > grid_x) grid_x = gx;
         }
     }
-    // One step in flight when every workgroup has a single tile (one matrix
-    // of at most a tile per CU: the MLA projections, a [1536 x 2048] call):
-    // such a call is bound by its first weight round trip, and a second
-    // step's loads only queue in front of the first one's (MLA Q8_0 decode
-    // 19.9 -> 19.2 us per layer). Larger launches keep two (HBM-bound).
-    const int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : (n == 1 && segs[0].tiles_per_wg == 1 ? 1 : 2);
+    // One step in flight when every workgroup has a single tile and each
+    // wave at most two steps (one matrix of at most a tile per CU: a
+    // [1536 x 2048] call, most MLA projections): both steps then go out at
+    // the start, and a deeper ring would only add out-of-range loads to the
+    // queue (MLA Q8_0 decode 19.9 -> 19.2 us per layer). Waves with three or
+    // more steps, and larger launches (HBM-bound), keep two.
+    const uint32_t chunk_steps = (min(segs[0].units, kChunkBlocks / 2) + ups - 1) / ups;
+    const bool short_waves = n == 1 && segs[0].tiles_per_wg == 1 && chunk_steps <= 2 * (uint32_t)(wg / 64);
+    const int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : (short_waves ? 1 : 2);
     if (route) return launch_q_set<1>(segs, 1, kernel_for<256, 2, true, 1>(ups), grid_x, 256, lds, s);
     if (n == 1) {
         const void* fn =
