@@ -78,8 +78,8 @@ __device__ __forceinline__ void quantize_planes(BufRsrc xr, BufRsrc ur, bool sil
 
 // Problem p of the launch: matrix, activation row and output row; false when
 // the problem does not run in this call.
-template <bool ROUTE>
-__device__ __forceinline__ bool select_problem(const GemvArgs& a, uint32_t p, uint64_t& mat, uint64_t& x_row,
+template <bool ROUTE, class A>
+__device__ __forceinline__ bool select_problem(const A& a, uint32_t p, uint64_t& mat, uint64_t& x_row,
                                                uint64_t& y_row) {
     mat = a.first_mat + p;
     x_row = p;
@@ -119,8 +119,29 @@ struct ItemPos {
 };
 
 
-template <int DEPTH, bool ROUTE, int NSEG, int WG = 1024>
-__global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
+// Arguments of a call with one segment, no problem list and no silu_mul
+// (a single matrix, or n_probs matrices and vectors at fixed strides), for
+// gemv_iq2_one_kernel: the fields the first loads depend on arrive as
+// scalar kernel arguments, which the hardware preloads into SGPRs (the
+// compiler preloads leading scalar arguments, not a struct), so no load
+// waits for a kernel-argument round trip; the rest is read from the
+// GemvArgs, where nothing needs it before the stores. recs and dvals already
+// point at the first matrix; strides are in 16-byte records, f16 scales and
+// floats.
+struct GemvOneArgs {
+    const uint4* recs;
+    const uint16_t* dvals;
+    const float* x;
+    uint32_t rec_stride, d_stride, x_stride;
+    uint32_t cols, units, tiles_per_wg, tiles, n_probs, d_row;
+    static constexpr uint64_t first_mat = 0, x2_off = 0;
+    static constexpr uint32_t silu_mul = 0;
+    static constexpr const uint4* probs = nullptr;
+    static constexpr const uint32_t* n_active = nullptr;
+};
+
+template <int DEPTH, bool ROUTE, int NSEG, int WG, class A>
+__device__ __forceinline__ void gemv_iq2_body(const A& a, const GemvArgs& lt) {
     using Shape = IqShape<WG>;
     constexpr bool kPair = Shape::kPair;
     constexpr uint32_t kWaves = Shape::kWaves;
@@ -149,10 +170,8 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
     uint8_t* const aq = lds.aq;
     float* const xs = lds.xs;
 
-    // This workgroup's segment (grid slice z) and problem within it (row y).
-    const GemvArgs& a = set.seg[NSEG > 1 ? blockIdx.z : 0];
+    // This workgroup's problem within its segment (row y); a: the segment.
     const uint32_t py = blockIdx.y;
-    pin_gemv_args(a);
     const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
     // The grid is sized for the widest and longest segment.
     if (t_begin >= a.tiles || py >= a.n_probs) return;  // whole workgroup
@@ -253,7 +272,7 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
             mat = sel;
             y_row = lds.sel[1];
         }
-        y_base = a.y + y_row * a.y_stride;
+        y_base = lt.y + y_row * lt.y_stride;
         rec_r = make_rsrc(a.recs + mat * a.rec_stride, (uint32_t)(a.rec_stride * 16));
         d_r = make_rsrc(a.dvals + mat * a.d_stride, (uint32_t)(a.d_stride * 2));
         start_chunk(0, uc0);
@@ -394,8 +413,28 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
     }
     if (threadIdx.x < n_tiles * 16) {
         const uint32_t row = (t_begin + (threadIdx.x >> 4)) * 16 + (threadIdx.x & 15);
-        if (row < a.rows) y_base[row] = row_acc;
+        if (row < lt.rows) y_base[row] = row_acc;
     }
+}
+
+template <int DEPTH, bool ROUTE, int NSEG, int WG = 1024>
+__global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kernel(GemvSet<NSEG> set) {
+    // This workgroup's segment (grid slice z).
+    const GemvArgs& a = set.seg[NSEG > 1 ? blockIdx.z : 0];
+    pin_gemv_args(a);
+    gemv_iq2_body<DEPTH, ROUTE, NSEG, WG>(a, a);
+}
+
+// One segment without a problem list or silu_mul (GemvOneArgs): the leading
+// scalar arguments (14 dwords: tiles per workgroup and problems share one)
+// are preloaded into SGPRs.
+template <int DEPTH, int WG>
+__global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_one_kernel(
+    const uint4* recs, const uint16_t* dvals, const float* x, uint32_t rec_stride, uint32_t d_stride, uint32_t x_stride,
+    uint32_t cols, uint32_t units, uint32_t tpw_probs, uint32_t tiles, uint32_t d_row, GemvSet<1> set) {
+    const GemvOneArgs a{recs,  dvals, x,     rec_stride,      d_stride,         x_stride, cols,
+                        units, tpw_probs & 0xFFFFu, tiles, tpw_probs >> 16, d_row};
+    gemv_iq2_body<DEPTH, false, 1, WG>(a, set.seg[0]);
 }
 
 static int env_int(const char* name, int dflt) {
@@ -671,7 +710,25 @@ hipError_t launch_gemv_iq2(const GemvArgs* segs_in, uint32_t n_segs, int num_cu,
                          : n == 1 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<1, false, 1, 768>)
                          : n == 2 ? reinterpret_cast<const void*>(&gemv_iq2_kernel<1, false, 2, 768>)
                                   : reinterpret_cast<const void*>(&gemv_iq2_kernel<1, false, 4, 768>);
-        if (n == 1) return launch_set<1>(segs, 1, fn, grid_x, 768, s);
+        if (n == 1) {
+            const GemvArgs& a = segs[0];
+            if (!route && !a.probs && !a.n_active && !a.silu_mul && a.rec_stride < (1ull << 27) &&
+                a.d_stride < (1ull << 30) && a.x_stride < (1ull << 32) && a.n_probs < 65536 && a.tiles_per_wg < 65536) {
+                // Preloaded arguments (gemv_iq2_one_kernel).
+                GemvSet<1> set{};
+                set.seg[0] = a;
+                const uint4* recs = a.recs + a.first_mat * a.rec_stride;
+                const uint16_t* dvals = a.dvals + a.first_mat * a.d_stride;
+                const float* x = a.x;
+                uint32_t rs = (uint32_t)a.rec_stride, ds = (uint32_t)a.d_stride, xs = (uint32_t)a.x_stride;
+                uint32_t cols = a.cols, units = a.units, tpw_np = a.tiles_per_wg | (a.n_probs << 16), tiles = a.tiles,
+                         drow = a.d_row;
+                void* args[] = {&recs, &dvals, &x, &rs, &ds, &xs, &cols, &units, &tpw_np, &tiles, &drow, &set};
+                return hipLaunchKernel(reinterpret_cast<const void*>(&gemv_iq2_one_kernel<1, 768>),
+                                       dim3(grid_x, a.n_probs, 1), dim3(768), args, 0, s);
+            }
+            return launch_set<1>(segs, 1, fn, grid_x, 768, s);
+        }
         if (n == 2) return launch_set<2>(segs, 2, fn, grid_x, 768, s);
         return launch_set<4>(segs, n, fn, grid_x, 768, s);
     }
