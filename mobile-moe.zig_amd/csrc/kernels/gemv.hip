@@ -55,8 +55,8 @@ struct StepPos {
 // in flight while LDS is filled. The stream runs one step ahead (two register
 // buffers): the CU's queue holds about one step per wave, and a deeper
 // prefetch only blocks the issuing wave.
-template <int UPS, int WG, int DEPTH, bool ROUTE, int NSEG>
-__global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set) {
+template <int UPS, int WG, int DEPTH, bool ROUTE, int NSEG, class A>
+__device__ __forceinline__ void gemv_q_body(const A& a, const GemvArgs& lt) {
     constexpr int FMT = kFmtQ8;
     constexpr uint32_t kWaves = WG / 64;
     constexpr int kRing = DEPTH + 1;  // register buffers: the step computing + DEPTH in flight
@@ -64,9 +64,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
     __shared__ float row_sum[kGemvMaxTiles * 16];
     __shared__ float edge[2][kWaves * 16];
     extern __shared__ __align__(16) uint8_t smem[];
-    // This workgroup's segment (grid slice z) and problem within it (row y).
-    const GemvArgs& a = set.seg[NSEG > 1 ? blockIdx.z : 0];
-    pin_gemv_args(a);
+    // a: this workgroup's segment; its problem is grid row y.
     const uint32_t t_begin = blockIdx.x * a.tiles_per_wg;
     // The grid is sized for the widest and longest segment.
     if (t_begin >= a.tiles || blockIdx.y >= a.n_probs) return;  // whole workgroup
@@ -106,7 +104,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
         if (!read_problem(a.probs, a.n_active, p, mat, x_row, y_row)) return;  // whole workgroup: not in this call
     }
     const float* x = a.x + x_row * a.x_stride;
-    float* const y_base = a.y + y_row * a.y_stride;
+    float* const y_base = lt.y + y_row * lt.y_stride;
     const bool silu_mul = a.silu_mul != 0;
     const uint32_t n_tiles = min(a.tiles - t_begin, a.tiles_per_wg);
     const bool has_a = n < 2;
@@ -253,7 +251,7 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
             }
             if (last) {
                 const uint32_t row = (t_begin + t) * 16 + rr;
-                if (row < a.rows) y_base[row] = v;
+                if (row < lt.rows) y_base[row] = v;
             }
         }
         if (last) break;
@@ -269,6 +267,25 @@ __global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set
         start_chunk(nb);
         issue_first();
     }
+}
+
+template <int UPS, int WG, int DEPTH, bool ROUTE, int NSEG>
+__global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_kernel(GemvSet<NSEG> set) {
+    // This workgroup's segment (grid slice z).
+    const GemvArgs& a = set.seg[NSEG > 1 ? blockIdx.z : 0];
+    pin_gemv_args(a);
+    gemv_q_body<UPS, WG, DEPTH, ROUTE, NSEG>(a, a);
+}
+
+// One segment without a problem list or silu_mul (GemvOneArgs, kernels.hpp):
+// the leading scalar arguments (14 dwords) are preloaded into SGPRs.
+template <int UPS, int WG, int DEPTH>
+__global__ __launch_bounds__(WG, 1024 / WG) void gemv_q_one_kernel(
+    const uint4* recs, const uint16_t* dvals, const float* x, uint32_t rec_stride, uint32_t d_stride, uint32_t x_stride,
+    uint32_t cols, uint32_t units, uint32_t tpw_probs, uint32_t tiles, uint32_t d_row, GemvSet<1> set) {
+    const GemvOneArgs a{recs,  dvals, x,     rec_stride,      d_stride,         x_stride, cols,
+                        units, tpw_probs & 0xFFFFu, tiles, tpw_probs >> 16, d_row};
+    gemv_q_body<UPS, WG, DEPTH, false, 1>(a, set.seg[0]);
 }
 
 // f32 / f16 weights (the router, matVecMulUnified's f32 branch): the
@@ -479,6 +496,15 @@ static const void* kernel_for_wg(int wg, int ups) {
     return kernel_for<256, DEPTH, false, 1>(ups);
 }
 
+template <int DEPTH>
+static const void* one_kernel_for(int wg, int ups) {
+    if (wg == 1024)
+        return ups == 8 ? reinterpret_cast<const void*>(&gemv_q_one_kernel<8, 1024, DEPTH>)
+                        : reinterpret_cast<const void*>(&gemv_q_one_kernel<4, 1024, DEPTH>);
+    return ups == 8 ? reinterpret_cast<const void*>(&gemv_q_one_kernel<8, 256, DEPTH>)
+                    : reinterpret_cast<const void*>(&gemv_q_one_kernel<4, 256, DEPTH>);
+}
+
 template <int N>
 static hipError_t launch_q_set(const GemvArgs* segs, uint32_t n_segs, const void* fn, uint32_t grid_x, int wg,
                                size_t lds, hipStream_t s) {
@@ -567,6 +593,24 @@ hipError_t launch_gemv_segments(const GemvArgs* segs_in, uint32_t n_segs, uint32
     const int depth = (depth_env >= 1 && depth_env <= 3) ? depth_env : (short_waves ? 1 : 2);
     if (route) return launch_q_set<1>(segs, 1, kernel_for<256, 2, true, 1>(ups), grid_x, 256, lds, s);
     if (n == 1) {
+        const GemvArgs& a = segs[0];
+        if (!a.probs && !a.n_active && !a.silu_mul && a.rec_stride < (1ull << 27) && a.d_stride < (1ull << 30) &&
+            a.x_stride < (1ull << 32) && a.n_probs < 65536 && a.tiles_per_wg < 65536) {
+            // Preloaded arguments (gemv_q_one_kernel).
+            const void* fn = depth == 1   ? one_kernel_for<1>(wg, ups)
+                             : depth == 3 ? one_kernel_for<3>(wg, ups)
+                                          : one_kernel_for<2>(wg, ups);
+            GemvSet<1> set{};
+            set.seg[0] = a;
+            const uint4* recs = a.recs + a.first_mat * a.rec_stride;
+            const uint16_t* dvals = a.dvals + a.first_mat * a.d_stride;
+            const float* x = a.x;
+            uint32_t rs = (uint32_t)a.rec_stride, ds = (uint32_t)a.d_stride, xs = (uint32_t)a.x_stride;
+            uint32_t cols = a.cols, units = a.units, tpw_np = a.tiles_per_wg | (a.n_probs << 16), tiles = a.tiles,
+                     drow = a.d_row;
+            void* args[] = {&recs, &dvals, &x, &rs, &ds, &xs, &cols, &units, &tpw_np, &tiles, &drow, &set};
+            return hipLaunchKernel(fn, dim3(grid_x, a.n_probs, 1), dim3(wg), args, lds, s);
+        }
         const void* fn =
             depth == 1 ? kernel_for_wg<1>(wg, ups) : depth == 3 ? kernel_for_wg<3>(wg, ups) : kernel_for_wg<2>(wg, ups);
         return launch_q_set<1>(segs, 1, fn, grid_x, wg, lds, s);

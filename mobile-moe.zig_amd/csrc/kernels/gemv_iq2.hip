@@ -119,27 +119,6 @@ struct ItemPos {
 };
 
 
-// Arguments of a call with one segment, no problem list and no silu_mul
-// (a single matrix, or n_probs matrices and vectors at fixed strides), for
-// gemv_iq2_one_kernel: the fields the first loads depend on arrive as
-// scalar kernel arguments, which the hardware preloads into SGPRs (the
-// compiler preloads leading scalar arguments, not a struct), so no load
-// waits for a kernel-argument round trip; the rest is read from the
-// GemvArgs, where nothing needs it before the stores. recs and dvals already
-// point at the first matrix; strides are in 16-byte records, f16 scales and
-// floats.
-struct GemvOneArgs {
-    const uint4* recs;
-    const uint16_t* dvals;
-    const float* x;
-    uint32_t rec_stride, d_stride, x_stride;
-    uint32_t cols, units, tiles_per_wg, tiles, n_probs, d_row;
-    static constexpr uint64_t first_mat = 0, x2_off = 0;
-    static constexpr uint32_t silu_mul = 0;
-    static constexpr const uint4* probs = nullptr;
-    static constexpr const uint32_t* n_active = nullptr;
-};
-
 template <int DEPTH, bool ROUTE, int NSEG, int WG, class A>
 __device__ __forceinline__ void gemv_iq2_body(const A& a, const GemvArgs& lt) {
     using Shape = IqShape<WG>;
@@ -427,7 +406,7 @@ __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_kerne
 
 // One segment without a problem list or silu_mul (GemvOneArgs): the leading
 // scalar arguments (14 dwords: tiles per workgroup and problems share one)
-// are preloaded into SGPRs.
+// are preloaded into SGPRs (GemvOneArgs, kernels.hpp).
 template <int DEPTH, int WG>
 __global__ __launch_bounds__(WG, IqShape<WG>::kPair ? 6 : 1) void gemv_iq2_one_kernel(
     const uint4* recs, const uint16_t* dvals, const float* x, uint32_t rec_stride, uint32_t d_stride, uint32_t x_stride,

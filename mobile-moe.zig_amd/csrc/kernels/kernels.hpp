@@ -99,6 +99,28 @@ struct GemvArgs {
 };
 
 
+// Arguments of a call with one segment, no problem list and no silu_mul
+// (a single matrix, or n_probs matrices and vectors at fixed strides), for
+// the decode GEMVs' *_one_kernel entries: the fields the first loads depend
+// on arrive as scalar kernel arguments, which the hardware preloads into
+// SGPRs (the
+// compiler preloads leading scalar arguments, not a struct), so no load
+// waits for a kernel-argument round trip; the rest is read from the
+// GemvArgs, where nothing needs it before the stores. recs and dvals already
+// point at the first matrix; strides are in 16-byte records, f16 scales and
+// floats.
+struct GemvOneArgs {
+    const uint4* recs;
+    const uint16_t* dvals;
+    const float* x;
+    uint32_t rec_stride, d_stride, x_stride;
+    uint32_t cols, units, tiles_per_wg, tiles, n_probs, d_row;
+    static constexpr uint64_t first_mat = 0, x2_off = 0;
+    static constexpr uint32_t silu_mul = 0;
+    static constexpr const uint4* probs = nullptr;
+    static constexpr const uint32_t* n_active = nullptr;
+};
+
 // Raw GGUF bytes -> f32, bit-exact (dequant.zig:316-390, 632-659).
 hipError_t launch_dequant(const void* raw, uint32_t ggml_type, uint64_t n, float* out, hipStream_t s);
 
